@@ -1,0 +1,455 @@
+// hip_backend.hip -- host side of libluxgpu_backend_hip.so.
+//
+// Implements the Lux GPU backend plugin ABI v2 (include/lux_gpu_backend_abi.h,
+// layout-identical to reference include/lux/gpu/backend_plugin.h) over HIP:
+//   context = one gfx950 device + one non-blocking stream,
+//   buffer  = one hipMalloc allocation,
+// and the additive quantized-matmul extension (include/lux_gpu_quant_backend.h).
+//
+// Semantics follow the reference's built-in CPU backend where the ABI leaves
+// them open (reference src/cpu_backend.cpp:121-165): buffer_alloc zero-fills,
+// copies move min(bytes, buffer size) bytes and succeed, copy-to-host blocks
+// and is ordered after all work queued on the context (the reference core
+// reads results without calling sync first, src/gpu_core.cpp:399-403).
+// No C++ exception crosses the C ABI.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+#include "../../include/lux_gpu_backend_abi.h"
+#include "../../include/lux_gpu_quant_backend.h"
+#include "kernels.h"
+
+namespace {
+
+struct HipContext {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    char name[256] = {0};
+    int compute_units = 0;
+    int max_wg = 0;
+};
+
+struct HipBuffer {
+    void* ptr = nullptr;
+    size_t size = 0;
+};
+
+HipContext* C(LuxBackendContext* c) { return reinterpret_cast<HipContext*>(c); }
+HipBuffer* B(LuxBackendBuffer* b) { return reinterpret_cast<HipBuffer*>(b); }
+
+LuxBackendError map_err(hipError_t e) {
+    switch (e) {
+    case hipSuccess: return LUX_BACKEND_OK;
+    case hipErrorOutOfMemory: return LUX_BACKEND_ERROR_OUT_OF_MEMORY;
+    case hipErrorInvalidValue: return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    case hipErrorNoDevice:
+    case hipErrorInvalidDevice: return LUX_BACKEND_ERROR_DEVICE_LOST;
+    default: return LUX_BACKEND_ERROR_INTERNAL;
+    }
+}
+
+LuxBackendError map_status(lxq::LuxStatus s) {
+    switch (s) {
+    case lxq::LuxStatus::Ok: return LUX_BACKEND_OK;
+    case lxq::LuxStatus::Invalid: return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    case lxq::LuxStatus::OutOfMemory: return LUX_BACKEND_ERROR_OUT_OF_MEMORY;
+    case lxq::LuxStatus::NotSupported: return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    default: return LUX_BACKEND_ERROR_INTERNAL;
+    }
+}
+
+bool is_gfx950(int dev) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return false;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// lifecycle, device info, sync
+// ---------------------------------------------------------------------------
+
+LuxBackendContext* hip_create_context(int device_index) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device_index < 0 || device_index >= count)
+        return nullptr;
+    if (!is_gfx950(device_index)) return nullptr;
+    if (hipSetDevice(device_index) != hipSuccess) return nullptr;
+    HipContext* ctx = new (std::nothrow) HipContext();
+    if (!ctx) return nullptr;
+    ctx->device = device_index;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device_index) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return nullptr;
+    }
+    std::snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", p.name, p.gcnArchName);
+    ctx->compute_units = p.multiProcessorCount;
+    ctx->max_wg = p.maxThreadsPerBlock;
+    return reinterpret_cast<LuxBackendContext*>(ctx);
+}
+
+void hip_destroy_context(LuxBackendContext* c) {
+    HipContext* ctx = C(c);
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) {
+        hipStreamSynchronize(ctx->stream);
+        hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+}
+
+LuxBackendError hip_get_device_count(int* count) {
+    if (!count) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    int ok = 0;
+    for (int d = 0; d < n; d++) ok += is_gfx950(d) ? 1 : 0;
+    *count = ok;
+    return LUX_BACKEND_OK;
+}
+
+LuxBackendError hip_get_device_info(LuxBackendContext* c, LuxBackendDeviceInfo* info) {
+    HipContext* ctx = C(c);
+    if (!ctx || !info) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    hipSetDevice(ctx->device);
+    size_t free_b = 0, total_b = 0;
+    hipError_t e = hipMemGetInfo(&free_b, &total_b);
+    if (e != hipSuccess) return map_err(e);
+    info->name = ctx->name;
+    info->vendor = "AMD";
+    info->memory_total = total_b;
+    info->memory_available = free_b;
+    info->compute_units = ctx->compute_units;
+    info->max_workgroup_size = ctx->max_wg;
+    info->is_discrete = true;
+    info->is_unified_memory = false;
+    return LUX_BACKEND_OK;
+}
+
+LuxBackendError hip_sync(LuxBackendContext* c) {
+    HipContext* ctx = C(c);
+    if (!ctx) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    return map_err(hipStreamSynchronize(ctx->stream));
+}
+
+// ---------------------------------------------------------------------------
+// buffers
+// ---------------------------------------------------------------------------
+
+LuxBackendBuffer* hip_buffer_alloc(LuxBackendContext* c, size_t bytes) {
+    HipContext* ctx = C(c);
+    if (!ctx) return nullptr;
+    hipSetDevice(ctx->device);
+    HipBuffer* b = new (std::nothrow) HipBuffer();
+    if (!b) return nullptr;
+    b->size = bytes;
+    if (bytes) {
+        if (hipMalloc(&b->ptr, bytes) != hipSuccess) {
+            delete b;
+            return nullptr;
+        }
+        // zero-filled like the reference CPU backend (src/cpu_backend.cpp:129);
+        // ordered before any later work on the context stream
+        if (hipMemsetAsync(b->ptr, 0, bytes, ctx->stream) != hipSuccess) {
+            hipFree(b->ptr);
+            delete b;
+            return nullptr;
+        }
+    }
+    return reinterpret_cast<LuxBackendBuffer*>(b);
+}
+
+LuxBackendBuffer* hip_buffer_alloc_with_data(LuxBackendContext* c, const void* data, size_t bytes) {
+    HipContext* ctx = C(c);
+    if (!ctx || (bytes && !data)) return nullptr;
+    hipSetDevice(ctx->device);
+    HipBuffer* b = new (std::nothrow) HipBuffer();
+    if (!b) return nullptr;
+    b->size = bytes;
+    if (bytes) {
+        if (hipMalloc(&b->ptr, bytes) != hipSuccess) {
+            delete b;
+            return nullptr;
+        }
+        // the caller may free `data` on return: copy synchronously
+        if (hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+            hipStreamSynchronize(ctx->stream) != hipSuccess) {
+            hipFree(b->ptr);
+            delete b;
+            return nullptr;
+        }
+    }
+    return reinterpret_cast<LuxBackendBuffer*>(b);
+}
+
+void hip_buffer_free(LuxBackendContext* c, LuxBackendBuffer* buf) {
+    HipBuffer* b = B(buf);
+    if (!b) return;
+    if (HipContext* ctx = C(c)) {
+        hipSetDevice(ctx->device);
+        // queued kernels may still read the buffer
+        hipStreamSynchronize(ctx->stream);
+    }
+    if (b->ptr) hipFree(b->ptr);
+    delete b;
+}
+
+LuxBackendError hip_buffer_copy_to_host(LuxBackendContext* c, LuxBackendBuffer* buf, void* dst,
+                                        size_t bytes) {
+    HipContext* ctx = C(c);
+    HipBuffer* b = B(buf);
+    if (!ctx || !b || !dst) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    const size_t n = std::min(bytes, b->size);
+    if (!n) return LUX_BACKEND_OK;
+    hipSetDevice(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, b->ptr, n, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return map_err(e);
+}
+
+LuxBackendError hip_buffer_copy_from_host(LuxBackendContext* c, LuxBackendBuffer* buf,
+                                          const void* src, size_t bytes) {
+    HipContext* ctx = C(c);
+    HipBuffer* b = B(buf);
+    if (!ctx || !b || !src) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    const size_t n = std::min(bytes, b->size);
+    if (!n) return LUX_BACKEND_OK;
+    hipSetDevice(ctx->device);
+    hipError_t e = hipMemcpyAsync(b->ptr, src, n, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return map_err(e);
+}
+
+void* hip_buffer_get_host_ptr(LuxBackendContext*, LuxBackendBuffer*) {
+    return nullptr;  // discrete device memory: no host view
+}
+
+// ---------------------------------------------------------------------------
+// quantized matmul extension
+// ---------------------------------------------------------------------------
+
+size_t dtype_size(int dt) { return dt == LUX_DTYPE_FLOAT32 ? 4 : 2; }
+bool dtype_ok(int dt) {
+    return dt == LUX_DTYPE_FLOAT32 || dt == LUX_DTYPE_FLOAT16 || dt == LUX_DTYPE_BFLOAT16;
+}
+bool bits_ok(int b) { return b == 2 || b == 3 || b == 4 || b == 5 || b == 6 || b == 8; }
+
+// shared shape/format validation: OK, INVALID_ARGUMENT or NOT_SUPPORTED
+LuxBackendError check_format(int K, int N, int group_size, int bits) {
+    if (K <= 0 || N < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (!bits_ok(bits)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    if (group_size != 32 && group_size != 64 && group_size != 128)
+        return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    if (K % group_size) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    return LUX_BACKEND_OK;
+}
+
+bool fits(HipBuffer* b, size_t need) { return b && (need == 0 || (b->ptr && b->size >= need)); }
+
+// M up to this value goes to the GEMV; LUX_HIP_GEMV_MAX_M overrides
+int gemv_max_m() {
+    static const int v = [] {
+        const char* e = std::getenv("LUX_HIP_GEMV_MAX_M");
+        int d = 8;
+        if (e && *e) d = std::atoi(e);
+        return d < 0 ? 0 : d;
+    }();
+    return v;
+}
+
+LuxQuantKernel select_kernel_impl(int M, int K, int N, int group_size, int bits,
+                                  LuxBackendDtype x_dtype) {
+    (void)N; (void)group_size; (void)bits;
+    if (x_dtype == LUX_DTYPE_FLOAT32 || K % 64 != 0) return LUX_QMM_KERNEL_GEMV;
+    return M <= gemv_max_m() ? LUX_QMM_KERNEL_GEMV : LUX_QMM_KERNEL_GEMM;
+}
+
+LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBuffer* w_q,
+                         LuxBackendBuffer* scales, LuxBackendBuffer* biases,
+                         LuxBackendBuffer* out, int M, int K, int N, int group_size, int bits,
+                         LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype,
+                         LuxBackendDtype out_dtype, LuxQuantKernel kernel) {
+    HipContext* ctx = C(c);
+    if (!ctx || !x || !w_q || !scales || !biases || !out) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (M < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    LuxBackendError e = check_format(K, N, group_size, bits);
+    if (e != LUX_BACKEND_OK) return e;
+    if (!dtype_ok(x_dtype) || !dtype_ok(sb_dtype) || !dtype_ok(out_dtype))
+        return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    if (kernel != LUX_QMM_KERNEL_AUTO && kernel != LUX_QMM_KERNEL_GEMV && kernel != LUX_QMM_KERNEL_GEMM)
+        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    const size_t G = (size_t)(K / group_size);
+    if (!fits(B(x), (size_t)M * K * dtype_size(x_dtype)) ||
+        !fits(B(w_q), (size_t)N * K * bits / 8) || !fits(B(scales), (size_t)N * G * dtype_size(sb_dtype)) ||
+        !fits(B(biases), (size_t)N * G * dtype_size(sb_dtype)) ||
+        !fits(B(out), (size_t)M * N * dtype_size(out_dtype)))
+        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (M == 0 || N == 0) return LUX_BACKEND_OK;
+
+    lxq::QmmArgs a;
+    a.x = B(x)->ptr;
+    a.wq = static_cast<const uint32_t*>(B(w_q)->ptr);
+    a.scales = B(scales)->ptr;
+    a.biases = B(biases)->ptr;
+    a.y = B(out)->ptr;
+    a.M = M; a.K = K; a.N = N; a.group_size = group_size; a.bits = bits;
+    a.x_dtype = x_dtype; a.sb_dtype = sb_dtype; a.out_dtype = out_dtype;
+
+    if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
+    if (kernel == LUX_QMM_KERNEL_AUTO) kernel = select_kernel_impl(M, K, N, group_size, bits, x_dtype);
+    if (kernel == LUX_QMM_KERNEL_GEMM) {
+        if (x_dtype == LUX_DTYPE_FLOAT32) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+        if (K % 64 == 0) {
+            lxq::LuxStatus s = lxq::launch_qgemm(a, ctx->stream);
+            if (s != lxq::LuxStatus::NotSupported) return map_status(s);
+        }
+        // shapes the GEMM tiling cannot take fall through to the GEMV
+    }
+    if (K % 64 == 0) {
+        lxq::LuxStatus s = lxq::launch_qgemv(a, ctx->stream);
+        if (s != lxq::LuxStatus::NotSupported) return map_status(s);
+    }
+    return map_status(lxq::launch_qmm_generic(a, ctx->stream));
+}
+
+LuxBackendError hip_op_quantized_matmul(LuxBackendContext* c, LuxBackendBuffer* x,
+                                        LuxBackendBuffer* w_q, LuxBackendBuffer* scales,
+                                        LuxBackendBuffer* biases, LuxBackendBuffer* out, int M,
+                                        int K, int N, int group_size, int bits,
+                                        LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype,
+                                        LuxBackendDtype out_dtype) {
+    return qmm_impl(c, x, w_q, scales, biases, out, M, K, N, group_size, bits, x_dtype, sb_dtype,
+                    out_dtype, LUX_QMM_KERNEL_AUTO);
+}
+
+LuxBackendError hip_op_quantized_matmul_ex(LuxBackendContext* c, LuxBackendBuffer* x,
+                                           LuxBackendBuffer* w_q, LuxBackendBuffer* scales,
+                                           LuxBackendBuffer* biases, LuxBackendBuffer* out,
+                                           int M, int K, int N, int group_size, int bits,
+                                           LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype,
+                                           LuxBackendDtype out_dtype, LuxQuantKernel kernel) {
+    return qmm_impl(c, x, w_q, scales, biases, out, M, K, N, group_size, bits, x_dtype, sb_dtype,
+                    out_dtype, kernel);
+}
+
+LuxBackendError hip_op_dequantize(LuxBackendContext* c, LuxBackendBuffer* w_q,
+                                  LuxBackendBuffer* scales, LuxBackendBuffer* biases,
+                                  LuxBackendBuffer* out, int N, int K, int group_size, int bits,
+                                  LuxBackendDtype sb_dtype, LuxBackendDtype out_dtype) {
+    HipContext* ctx = C(c);
+    if (!ctx || !w_q || !scales || !biases || !out) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    LuxBackendError e = check_format(K, N, group_size, bits);
+    if (e != LUX_BACKEND_OK) return e;
+    if (!dtype_ok(sb_dtype) || !dtype_ok(out_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    const size_t G = (size_t)(K / group_size);
+    if (!fits(B(w_q), (size_t)N * K * bits / 8) || !fits(B(scales), (size_t)N * G * dtype_size(sb_dtype)) ||
+        !fits(B(biases), (size_t)N * G * dtype_size(sb_dtype)) ||
+        !fits(B(out), (size_t)N * K * dtype_size(out_dtype)))
+        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (N == 0) return LUX_BACKEND_OK;
+    if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
+    return map_status(lxq::launch_dequantize(static_cast<const uint32_t*>(B(w_q)->ptr), B(scales)->ptr,
+                                             B(biases)->ptr, B(out)->ptr, N, K, group_size, bits,
+                                             sb_dtype, out_dtype, ctx->stream));
+}
+
+LuxBackendError hip_op_quantize(LuxBackendContext* c, LuxBackendBuffer* w, LuxBackendBuffer* w_q,
+                                LuxBackendBuffer* scales, LuxBackendBuffer* biases, int N, int K,
+                                int group_size, int bits, LuxBackendDtype w_dtype,
+                                LuxBackendDtype sb_dtype) {
+    HipContext* ctx = C(c);
+    if (!ctx || !w || !w_q || !scales || !biases) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    LuxBackendError e = check_format(K, N, group_size, bits);
+    if (e != LUX_BACKEND_OK) return e;
+    if (!dtype_ok(w_dtype) || !dtype_ok(sb_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    const size_t G = (size_t)(K / group_size);
+    if (!fits(B(w), (size_t)N * K * dtype_size(w_dtype)) || !fits(B(w_q), (size_t)N * K * bits / 8) ||
+        !fits(B(scales), (size_t)N * G * dtype_size(sb_dtype)) ||
+        !fits(B(biases), (size_t)N * G * dtype_size(sb_dtype)))
+        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (N == 0) return LUX_BACKEND_OK;
+    if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
+    return map_status(lxq::launch_quantize(B(w)->ptr, static_cast<uint32_t*>(B(w_q)->ptr),
+                                           B(scales)->ptr, B(biases)->ptr, N, K, group_size, bits,
+                                           w_dtype, sb_dtype, ctx->stream));
+}
+
+void* hip_get_native_stream(LuxBackendContext* c) {
+    HipContext* ctx = C(c);
+    return ctx ? reinterpret_cast<void*>(ctx->stream) : nullptr;
+}
+
+LuxQuantKernel hip_select_kernel(int M, int K, int N, int group_size, int bits,
+                                 LuxBackendDtype x_dtype) {
+    return select_kernel_impl(M, K, N, group_size, bits, x_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// tables
+// ---------------------------------------------------------------------------
+
+lux_gpu_backend_vtbl make_vtbl() {
+    lux_gpu_backend_vtbl v;
+    std::memset(&v, 0, sizeof(v));  // every slot not set below is NOT_SUPPORTED
+    v.create_context = hip_create_context;
+    v.destroy_context = hip_destroy_context;
+    v.get_device_count = hip_get_device_count;
+    v.get_device_info = hip_get_device_info;
+    v.sync = hip_sync;
+    v.buffer_alloc = hip_buffer_alloc;
+    v.buffer_alloc_with_data = hip_buffer_alloc_with_data;
+    v.buffer_free = hip_buffer_free;
+    v.buffer_copy_to_host = hip_buffer_copy_to_host;
+    v.buffer_copy_from_host = hip_buffer_copy_from_host;
+    v.buffer_get_host_ptr = hip_buffer_get_host_ptr;
+    return v;
+}
+
+const lux_gpu_backend_vtbl g_vtbl = make_vtbl();
+
+lux_gpu_quant_vtbl make_qvtbl() {
+    lux_gpu_quant_vtbl q;
+    std::memset(&q, 0, sizeof(q));
+    q.ext_version = LUX_GPU_QUANT_EXT_VERSION;
+    q.struct_size = sizeof(lux_gpu_quant_vtbl);
+    q.op_quantized_matmul = hip_op_quantized_matmul;
+    q.op_dequantize = hip_op_dequantize;
+    q.op_quantize = hip_op_quantize;
+    q.op_quantized_matmul_ex = hip_op_quantized_matmul_ex;
+    q.get_native_stream = hip_get_native_stream;
+    q.select_kernel = hip_select_kernel;
+    return q;
+}
+
+const lux_gpu_quant_vtbl g_qvtbl = make_qvtbl();
+
+}  // namespace
+
+extern "C" __attribute__((visibility("default"))) bool lux_gpu_backend_init(lux_gpu_backend_desc* out) {
+    if (!out) return false;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return false;
+    bool any = false;
+    for (int d = 0; d < n && !any; d++) any = is_gfx950(d);
+    if (!any) return false;
+    out->abi_version = LUX_GPU_BACKEND_ABI_VERSION;
+    out->backend_name = "hip";
+    out->backend_version = "0.1.0";
+    // only buffers and the quantized extension: no base tensor-op slots are
+    // filled, so TENSOR_OPS / MATMUL are not advertised (and never UNIFIED_MEMORY)
+    out->capabilities = 0;
+    out->vtbl = &g_vtbl;
+    return true;
+}
+
+extern "C" __attribute__((visibility("default"))) bool lux_gpu_backend_quant_init(const lux_gpu_quant_vtbl** out) {
+    if (!out) return false;
+    *out = &g_qvtbl;
+    return true;
+}

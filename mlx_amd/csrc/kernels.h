@@ -1,0 +1,38 @@
+// kernels.h -- launchers of the gfx950 quantized-matmul kernels.  Host code
+// validates arguments and buffer sizes before calling these; the launchers
+// only check what their kernels' tiling assumes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace lxq {
+
+enum class LuxStatus : int { Ok = 0, Invalid = 1, OutOfMemory = 2, NotSupported = 3, Internal = 5 };
+
+struct QmmArgs {
+    const void* x;        // [M, K] x_dtype
+    const uint32_t* wq;   // [N, K*bits/32]
+    const void* scales;   // [N, K/group_size] sb_dtype
+    const void* biases;   // [N, K/group_size] sb_dtype
+    void* y;              // [M, N] out_dtype
+    int M, K, N, group_size, bits;
+    int x_dtype, sb_dtype, out_dtype;
+};
+
+// bandwidth-bound dequant-GEMV (any M; tuned for M <= 8); needs K % 64 == 0
+LuxStatus launch_qgemv(const QmmArgs& a, hipStream_t st);
+// MFMA GEMM for f16/bf16 activations; needs K % 64 == 0
+LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st);
+// generic one-thread-per-output kernel for shapes the tiled kernels reject
+LuxStatus launch_qmm_generic(const QmmArgs& a, hipStream_t st);
+
+// out[N, K] = dequant(w_q) in out_dtype
+LuxStatus launch_dequantize(const uint32_t* wq, const void* scales, const void* biases, void* out,
+                            int N, int K, int group_size, int bits, int sb_dtype, int out_dtype,
+                            hipStream_t st);
+// w[N, K] (w_dtype) -> w_q, scales, biases
+LuxStatus launch_quantize(const void* w, uint32_t* wq, void* scales, void* biases, int N, int K,
+                          int group_size, int bits, int w_dtype, int sb_dtype, hipStream_t st);
+
+}  // namespace lxq

@@ -1,0 +1,197 @@
+"""Host runtime over the HIP plugin's C ABI: contexts, device buffers, and
+the quantized ops, with numpy arrays on the host side.
+
+This is plumbing for tests and the benchmark; the product is the plugin
+library.  Every call goes through the vtable / quant-extension function
+pointers the plugin exported, exactly as a C or Go embedder would call them,
+and raises LuxError on a non-OK LuxBackendError.  There is no CPU fallback:
+if the plugin or its GPU is missing, get_backend() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import numpy as np
+
+from . import abi
+from .loader import LoadedBackend, PluginLoader
+
+_ESZ = {abi.FLOAT32: 4, abi.FLOAT16: 2, abi.BFLOAT16: 2}
+_NP = {abi.FLOAT32: np.float32, abi.FLOAT16: np.uint16, abi.BFLOAT16: np.uint16}
+
+
+class LuxError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what}: {abi.ERROR_NAMES.get(code, code)}")
+        self.code = code
+
+
+def _check(code: int, what: str) -> None:
+    if code != abi.OK:
+        raise LuxError(code, what)
+
+
+_backend: Optional[LoadedBackend] = None
+
+
+def get_backend(name: str = "hip") -> LoadedBackend:
+    """Load the named plugin through the loader (LUX_GPU_BACKEND_PATH, then
+    the default and in-tree plugin directories)."""
+    global _backend
+    if _backend is None:
+        L = PluginLoader()
+        if not L.load_backend(name):
+            raise RuntimeError(
+                f"backend '{name}' unavailable: libluxgpu_backend_{name}.so not found, "
+                "or no gfx950 device (searched: " + ", ".join(L.search_paths) + ")")
+        b = L.get_backend(name)
+        if b.quant is None:
+            raise RuntimeError(f"backend '{name}' has no quantized-matmul extension")
+        _backend = b
+    return _backend
+
+
+class Buffer:
+    def __init__(self, ctx: "Context", handle: int, nbytes: int):
+        self.ctx, self.handle, self.nbytes = ctx, handle, nbytes
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx.vt.buffer_free(self.ctx.handle, self.handle)
+            self.handle = None
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        _check(self.ctx.vt.buffer_copy_to_host(self.ctx.handle, self.handle,
+                                               out.ctypes.data, out.nbytes), "buffer_copy_to_host")
+        return out
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        _check(self.ctx.vt.buffer_copy_from_host(self.ctx.handle, self.handle,
+                                                 a.ctypes.data, a.nbytes), "buffer_copy_from_host")
+
+
+class Context:
+    def __init__(self, device_index: int = 0, backend: Optional[LoadedBackend] = None):
+        self.be = backend or get_backend()
+        self.vt = self.be.vtbl
+        self.q = self.be.quant
+        self.handle = self.vt.create_context(device_index)
+        if not self.handle:
+            raise RuntimeError(f"create_context({device_index}) failed")
+
+    def close(self) -> None:
+        if self.handle:
+            self.vt.destroy_context(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # --- buffers ---------------------------------------------------------
+    def alloc(self, nbytes: int) -> Buffer:
+        h = self.vt.buffer_alloc(self.handle, nbytes)
+        if not h:
+            raise LuxError(abi.ERR_OUT_OF_MEMORY, f"buffer_alloc({nbytes})")
+        return Buffer(self, h, nbytes)
+
+    def upload(self, a: np.ndarray) -> Buffer:
+        a = np.ascontiguousarray(a)
+        h = self.vt.buffer_alloc_with_data(self.handle, a.ctypes.data, a.nbytes)
+        if not h:
+            raise LuxError(abi.ERR_OUT_OF_MEMORY, f"buffer_alloc_with_data({a.nbytes})")
+        return Buffer(self, h, a.nbytes)
+
+    def sync(self) -> None:
+        _check(self.vt.sync(self.handle), "sync")
+
+    def device_info(self) -> abi.DeviceInfo:
+        info = abi.DeviceInfo()
+        _check(self.vt.get_device_info(self.handle, ctypes.byref(info)), "get_device_info")
+        return info
+
+    @property
+    def stream(self) -> int:
+        return self.q.get_native_stream(self.handle)
+
+    # --- quantized ops (asynchronous on the context stream) ---------------
+    def quantized_matmul(self, x: Buffer, w_q: Buffer, scales: Buffer, biases: Buffer, out: Buffer,
+                         M: int, K: int, N: int, group_size: int, bits: int, x_dtype: int,
+                         sb_dtype: int, out_dtype: int, kernel: int = abi.KERNEL_AUTO) -> None:
+        _check(self.q.op_quantized_matmul_ex(self.handle, x.handle, w_q.handle, scales.handle,
+                                             biases.handle, out.handle, M, K, N, group_size, bits,
+                                             x_dtype, sb_dtype, out_dtype, kernel),
+               "op_quantized_matmul")
+
+    def dequantize(self, w_q: Buffer, scales: Buffer, biases: Buffer, out: Buffer, N: int, K: int,
+                   group_size: int, bits: int, sb_dtype: int, out_dtype: int) -> None:
+        _check(self.q.op_dequantize(self.handle, w_q.handle, scales.handle, biases.handle,
+                                    out.handle, N, K, group_size, bits, sb_dtype, out_dtype),
+               "op_dequantize")
+
+    def quantize(self, w: Buffer, w_q: Buffer, scales: Buffer, biases: Buffer, N: int, K: int,
+                 group_size: int, bits: int, w_dtype: int, sb_dtype: int) -> None:
+        _check(self.q.op_quantize(self.handle, w.handle, w_q.handle, scales.handle, biases.handle,
+                                  N, K, group_size, bits, w_dtype, sb_dtype), "op_quantize")
+
+    def select_kernel(self, M, K, N, group_size, bits, x_dtype) -> int:
+        return self.q.select_kernel(M, K, N, group_size, bits, x_dtype)
+
+
+def esize(dtype: int) -> int:
+    return _ESZ[dtype]
+
+
+def np_dtype(dtype: int):
+    return _NP[dtype]
+
+
+def run_quantized_matmul(ctx: Context, x: np.ndarray, w_q: np.ndarray, scales: np.ndarray,
+                         biases: np.ndarray, M: int, K: int, N: int, group_size: int, bits: int,
+                         x_dtype: int, sb_dtype: int, out_dtype: int,
+                         kernel: int = abi.KERNEL_AUTO) -> np.ndarray:
+    """Upload, run one quantized matmul, download.  Host arrays in, host array out."""
+    bufs = [ctx.upload(a) for a in (x, w_q, scales, biases)]
+    out = ctx.alloc(max(1, M * N * esize(out_dtype)))
+    try:
+        ctx.quantized_matmul(*bufs, out, M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype,
+                             kernel)
+        return out.download(np_dtype(out_dtype), (M, N))
+    finally:
+        for b in bufs + [out]:
+            b.free()
+
+
+def run_dequantize(ctx: Context, w_q, scales, biases, K: int, group_size: int, bits: int,
+                   sb_dtype: int, out_dtype: int) -> np.ndarray:
+    N = w_q.shape[0]
+    bufs = [ctx.upload(a) for a in (w_q, scales, biases)]
+    out = ctx.alloc(max(1, N * K * esize(out_dtype)))
+    try:
+        ctx.dequantize(*bufs, out, N, K, group_size, bits, sb_dtype, out_dtype)
+        return out.download(np_dtype(out_dtype), (N, K))
+    finally:
+        for b in bufs + [out]:
+            b.free()
+
+
+def run_quantize(ctx: Context, w: np.ndarray, group_size: int, bits: int, w_dtype: int,
+                 sb_dtype: int) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    N, K = w.shape
+    G = K // group_size
+    wb = ctx.upload(w)
+    wq = ctx.alloc(N * K * bits // 8)
+    s = ctx.alloc(N * G * esize(sb_dtype))
+    b = ctx.alloc(N * G * esize(sb_dtype))
+    try:
+        ctx.quantize(wb, wq, s, b, N, K, group_size, bits, w_dtype, sb_dtype)
+        return (wq.download(np.uint32, (N, K * bits // 32)),
+                s.download(np_dtype(sb_dtype), (N, G)), b.download(np_dtype(sb_dtype), (N, G)))
+    finally:
+        for x in (wb, wq, s, b):
+            x.free()

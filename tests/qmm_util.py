@@ -1,0 +1,42 @@
+"""Shared helpers for the GPU parity tests: comparison gates and problem
+construction.  The gates are the tolerances the north star states:
+  fp32 output  max|d| / max|y| <= 1e-5
+  fp16 output  max|d| / max|y| <= 1e-3
+  bf16 output  every element within one bf16 ulp of the oracle's bf16 value
+               (bf16 rounding of the output alone is ~2e-3 of max|y|, so the
+               1e-3 form cannot hold for any implementation; the literal
+               metric is still computed and returned)
+"""
+import numpy as np
+
+F32, F16, BF16 = 0, 1, 2
+TOL = {F32: 1e-5, F16: 1e-3}
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max()
+    return float(np.abs(y - ref).max() / scale) if scale > 0 else float(np.abs(y - ref).max())
+
+
+def bf16_ulp(v):
+    """ulp of bf16 values (float32 input holding bf16 numbers)."""
+    a = np.abs(np.asarray(v, np.float32))
+    e = np.floor(np.log2(np.maximum(a, np.float32(2.0 ** -126))))
+    return np.float64(2.0) ** (e - 7)
+
+
+def check_output(O, y_gpu, y_cpu, out_dtype, what=""):
+    """y_gpu, y_cpu: raw arrays in out_dtype (uint16 bit patterns for 16-bit)."""
+    g = O.to_f32(y_gpu, out_dtype) if out_dtype != F32 else y_gpu
+    c = O.to_f32(y_cpu, out_dtype) if out_dtype != F32 else y_cpu
+    assert np.all(np.isfinite(g)), f"{what}: non-finite GPU output"
+    r = rel_err(g, c)
+    if out_dtype == BF16:
+        ulp = np.maximum(bf16_ulp(c), bf16_ulp(g))
+        bad = np.abs(g.astype(np.float64) - c.astype(np.float64)) > ulp * (1 + 1e-6)
+        assert not bad.any(), f"{what}: {bad.sum()} bf16 elements differ by more than 1 ulp (rel {r:.3g})"
+    else:
+        assert r <= TOL[out_dtype], f"{what}: max|d|/max|y| = {r:.3g} > {TOL[out_dtype]}"
+    return r

@@ -1,0 +1,201 @@
+"""The drop-in boundary, on the CPU: ABI layout, exported symbols, loader
+behaviour (reference src/plugin_loader.hpp) including its failure paths,
+forced with fake plugins.  No GPU calls."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+FAKE_SRC = os.path.join(ROOT, "tests", "fake_plugins", "fake_plugin.c")
+LAYOUT_SRC = os.path.join(ROOT, "tests", "fake_plugins", "abi_layout.c")
+REF_INCLUDE = "/root/reference/include"
+
+
+def _run(cmd, **kw):
+    r = subprocess.run(cmd, capture_output=True, text=True, **kw)
+    assert r.returncode == 0, f"{cmd}\n{r.stdout}\n{r.stderr}"
+    return r.stdout
+
+
+def declared_symbols():
+    """Functions the public headers declare with default visibility."""
+    syms = set()
+    for h in os.listdir(INCLUDE):
+        if h.endswith(".h"):
+            txt = open(os.path.join(INCLUDE, h)).read()
+            syms |= set(re.findall(r'visibility\("default"\)\)\)\s+\w+\s+(\w+)\s*\(', txt))
+    return syms
+
+
+def test_headers_compile_and_layout_asserts_hold(tmp_path):
+    for h in ("lux_gpu_backend_abi.h", "lux_gpu_quant_backend.h"):
+        src = tmp_path / "t.c"
+        src.write_text(f'#include "{INCLUDE}/{h}"\nint main(void){{return 0;}}\n')
+        _run(["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", str(src)])
+        _run(["g++", "-std=c++17", "-Wall", "-Werror", "-fsyntax-only", "-x", "c++", str(src)])
+
+
+def _layout(tmp_path, ref: bool):
+    exe = tmp_path / ("layout_ref" if ref else "layout")
+    cmd = ["gcc", "-std=c11", "-O0", LAYOUT_SRC, "-o", str(exe)]
+    if ref:
+        cmd[1:1] = ["-DUSE_REF", f"-I{REF_INCLUDE}"]
+    _run(cmd)
+    return [int(v) for v in _run([str(exe)]).split()]
+
+
+def test_abi_layout_matches_ctypes_mirror(tmp_path):
+    from mlx_amd import abi
+    got = _layout(tmp_path, ref=False)
+    names = [f[0] for f in abi.BackendVtbl._fields_]
+    assert len(names) == 61
+    assert got[:61] == [getattr(abi.BackendVtbl, n).offset for n in names]
+    assert got[61:] == [ctypes.sizeof(abi.BackendVtbl), ctypes.sizeof(abi.BackendDesc),
+                        abi.BackendDesc.vtbl.offset, ctypes.sizeof(abi.DeviceInfo), abi.ABI_VERSION]
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="reference headers not mounted")
+def test_abi_layout_identical_to_reference_header(tmp_path):
+    """Same slot offsets, struct sizes and ABI version as the reference's
+    include/lux/gpu/backend_plugin.h."""
+    assert _layout(tmp_path, ref=False) == _layout(tmp_path, ref=True)
+
+
+def test_plugin_exports_exactly_the_declared_symbols():
+    import mlx_amd
+    assert mlx_amd.plugin_built(), "run __graft_entry__.build() first"
+    out = _run(["nm", "-D", "--defined-only", mlx_amd.PLUGIN_PATH])
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    declared = declared_symbols()
+    assert declared == {"lux_gpu_backend_init", "lux_gpu_backend_quant_init"}
+    assert declared <= exported
+    # nothing else leaks from the plugin (hidden visibility)
+    assert {s for s in exported if s.startswith("lux")} == declared
+    # and the library loads; its symbols resolve through dlsym
+    lib = ctypes.CDLL(mlx_amd.PLUGIN_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    for s in declared:
+        assert getattr(lib, s) is not None
+
+
+def test_quant_extension_table_without_gpu():
+    """The extension table is static: usable for introspection without a device."""
+    import mlx_amd
+    from mlx_amd import abi
+    lib = ctypes.CDLL(mlx_amd.PLUGIN_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    qinit = abi.QUANT_INIT_FN(("lux_gpu_backend_quant_init", lib))
+    p = ctypes.POINTER(abi.QuantVtbl)()
+    assert qinit(ctypes.byref(p))
+    q = p.contents
+    assert q.ext_version == abi.QUANT_EXT_VERSION
+    assert q.struct_size == ctypes.sizeof(abi.QuantVtbl)
+    # kernel selection is pure host logic
+    assert q.select_kernel(1, 4096, 14336, 64, 4, abi.FLOAT16) == abi.KERNEL_GEMV
+    assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.BFLOAT16) == abi.KERNEL_GEMM
+    assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.FLOAT32) == abi.KERNEL_GEMV
+    # NULL context / buffers are rejected before any device work
+    assert q.op_quantized_matmul(None, None, None, None, None, None, 1, 64, 1, 64, 4, 1, 1, 1) == \
+        abi.ERR_INVALID_ARGUMENT
+    assert q.op_dequantize(None, None, None, None, None, 1, 64, 64, 4, 1, 1) == abi.ERR_INVALID_ARGUMENT
+
+
+# ------------------------------------------------------------- loader ------
+
+def _fake(tmp_path, name, *defs, subdir="p"):
+    d = tmp_path / subdir
+    d.mkdir(exist_ok=True)
+    so = d / f"libluxgpu_backend_{name}.so"
+    _run(["gcc", "-std=c11", "-shared", "-fPIC", f'-DFAKE_NAME="{name}"', *defs, FAKE_SRC,
+          "-o", str(so)])
+    return d, so
+
+
+def test_loader_accepts_good_plugin_and_orders_paths(tmp_path):
+    from mlx_amd.loader import PluginLoader
+    d1, _ = _fake(tmp_path, "metal", subdir="a")
+    env = {"LUX_GPU_BACKEND_PATH": f"/nonexistent:{d1}"}
+    L = PluginLoader(env)
+    # the last entry of the variable is searched first (reference :135-141)
+    assert L.search_paths[0] == str(d1) and L.search_paths[1] == "/nonexistent"
+    assert L.load_backend("metal")
+    b = L.get_backend("metal")
+    assert b.available and b.desc.abi_version == 2 and b.quant is None
+    assert L.available_backends() == ["cpu", "metal"]
+    assert L.get_best_backend() is b
+    assert not L.load_backend("webgpu")
+
+
+def test_loader_init_false_means_unavailable(tmp_path):
+    from mlx_amd.loader import PluginLoader
+    d, so = _fake(tmp_path, "cuda", "-DFAKE_INIT_FALSE")
+    L = PluginLoader({"LUX_GPU_BACKEND_PATH": str(d)})
+    assert not L.load_backend_from_path(str(so))
+    assert L.get_backend("cuda") is None and L.available_backends() == ["cpu"]
+
+
+def test_loader_rejects_abi_mismatch(tmp_path, capfd):
+    from mlx_amd.loader import PluginLoader
+    d, so = _fake(tmp_path, "webgpu", "-DFAKE_ABI=1")
+    L = PluginLoader({"LUX_GPU_BACKEND_PATH": str(d)})
+    assert not L.load_backend("webgpu")
+    assert "has ABI version 1, expected 2" in capfd.readouterr().err
+    assert L.backends == {}
+
+
+def test_context_failure_is_reported(tmp_path):
+    from mlx_amd import runtime
+    from mlx_amd.loader import PluginLoader
+    d, _ = _fake(tmp_path, "metal", "-DFAKE_NULL_CTX")
+    L = PluginLoader({"LUX_GPU_BACKEND_PATH": str(d)})
+    assert L.load_backend("metal")
+    b = L.get_backend("metal")
+    b.quant = object()  # the fake has no extension; only create_context matters here
+    with pytest.raises(RuntimeError, match="create_context"):
+        runtime.Context(0, backend=b)
+
+
+def test_lux_backend_selection(tmp_path):
+    from mlx_amd.loader import PluginLoader
+    d, _ = _fake(tmp_path, "metal")
+    _fake(tmp_path, "cuda")
+    env = {"LUX_GPU_BACKEND_PATH": str(d)}
+    assert PluginLoader(dict(env, LUX_BACKEND="cuda")).select().name == "cuda"
+    assert PluginLoader(dict(env)).select().name == "metal"          # priority order
+    assert PluginLoader(dict(env, LUX_BACKEND="cpu")).select() is None
+    assert PluginLoader(dict(env, LUX_BACKEND="webgpu")).select() is None
+
+
+def test_hip_plugin_without_gpu_reports_unavailable():
+    """On a machine with no gfx950 device the plugin's init returns false, the
+    loader registers it unavailable, and the runtime refuses to run (no CPU
+    fallback)."""
+    import torch  # noqa: F401  (only to know whether a GPU is visible)
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    from mlx_amd import runtime
+    from mlx_amd.loader import PluginLoader
+    L = PluginLoader({})
+    assert not L.load_backend("hip")
+    runtime._backend = None
+    with pytest.raises(RuntimeError, match="unavailable"):
+        runtime.get_backend("hip")
+
+
+def test_reference_loader_loads_plugins(tmp_path):
+    """The reference's own PluginLoader (compiled from its header into
+    oracle/_ref) accepts a plugin built against this project's ABI header."""
+    probe = os.path.join(ROOT, "oracle", "_ref", "ref_loader_probe")
+    if not os.path.exists(probe):
+        pytest.skip("oracle/_ref not built")
+    import json
+    d, _ = _fake(tmp_path, "metal")
+    out = json.loads(_run([probe, "metal"], env=dict(os.environ, LUX_GPU_BACKEND_PATH=str(d))))
+    assert out["loaded"] and out["available"] and out["abi_version"] == 2
+    assert out["backend_name"] == "metal" and out["context"]
+    d2, _ = _fake(tmp_path, "cuda", "-DFAKE_ABI=1", subdir="q")
+    out = json.loads(_run([probe, "cuda"], env=dict(os.environ, LUX_GPU_BACKEND_PATH=str(d2))))
+    assert not out["available"]

@@ -1,0 +1,192 @@
+"""GPU parity: the HIP plugin, called through its C ABI, against the CPU
+oracle on the same seeded inputs.
+
+Bit-exact: dequantize (fp32 output), quantize (codes, scales, biases).
+Tolerance (qmm_util): quantized matmul on every kernel path.
+Full BASELINE shapes: exact comparison for the decode/crossover/irregular
+configs; the prefill GEMM (M=2048) is checked on a seeded sample of rows,
+which the oracle finishes in seconds.
+"""
+import numpy as np
+import pytest
+
+from qmm_util import BF16, F16, F32, check_output
+
+pytestmark = pytest.mark.gpu
+
+BITS = [2, 3, 4, 5, 6, 8]
+KERNELS = {"auto": 0, "gemv": 1, "gemm": 2}
+
+
+def run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, kernel=0):
+    from mlx_amd import runtime
+    print(f"[case] qmm M={M} K={K} N={N} g={gs} bits={bits} x={xd} sb={sbd} out={od} kernel={kernel}",
+          flush=True)
+    return runtime.run_quantized_matmul(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, kernel)
+
+
+def test_device_and_buffers(ctx):
+    info = ctx.device_info()
+    assert b"gfx950" in info.name and info.is_discrete and not info.is_unified_memory
+    assert info.compute_units >= 200 and info.memory_total > 100 * 2**30
+    # buffer_alloc zero-fills; copies move min(bytes, size) bytes
+    buf = ctx.alloc(64)
+    assert np.all(buf.download(np.uint8, (64,)) == 0)
+    big = np.arange(100, dtype=np.uint8)
+    buf.upload(big)                       # 100 bytes into a 64-byte buffer
+    out = np.full(80, 7, np.uint8)
+    from mlx_amd import runtime
+    runtime._check(ctx.vt.buffer_copy_to_host(ctx.handle, buf.handle, out.ctypes.data, 80), "copy")
+    assert np.array_equal(out[:64], big[:64]) and np.all(out[64:] == 7)
+    buf.free()
+    ctx.sync()
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("sb", [F32, F16, BF16])
+def test_dequantize_bit_exact(ctx, oracle, bits, sb):
+    from mlx_amd import runtime
+    O = oracle
+    N, K, gs = 37, 512, 64 if bits != 8 else 128
+    w = O.rng_normal(N * K, 500 + bits, 0.0, 0.02).reshape(N, K)
+    w_q, s, b = O.quantize(w, gs, bits, sb)
+    for od in (F32, F16, BF16):
+        print(f"[case] dequant bits={bits} sb={sb} out={od}", flush=True)
+        got = runtime.run_dequantize(ctx, w_q, s, b, K, gs, bits, sb, od)
+        want = O.dequantize(w_q, s, b, K, gs, bits, sb, od)
+        assert np.array_equal(got.view(np.uint16 if od else np.uint32),
+                              want.view(np.uint16 if od else np.uint32))
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantize_bit_exact(ctx, oracle, bits, gs):
+    from mlx_amd import runtime
+    O = oracle
+    N, K = 29, 512
+    w = O.rng_normal(N * K, 900 + bits, 0.0, 0.02).reshape(N, K)
+    w[0, :gs] = -0.5  # constant group
+    w.reshape(-1)[::97] *= 20.0  # outliers
+    for sb in (F32, F16, BF16):
+        print(f"[case] quantize bits={bits} g={gs} sb={sb}", flush=True)
+        gq, gs_, gb = runtime.run_quantize(ctx, w, gs, bits, F32, sb)
+        wq, s, b = O.quantize(w, gs, bits, sb)
+        assert np.array_equal(gq, wq)
+        assert np.array_equal(gs_, s) and np.array_equal(gb, b)
+
+
+# ---- GEMV ---------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F32, F32, F32),
+                                       (F16, F32, F32), (BF16, F16, F32)])
+def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
+    O = oracle
+    for (M, K, N, gs) in [(1, 4096, 300, 64), (3, 1024, 129, 32), (8, 512, 77, 128),
+                          (5, 8192, 64, 64), (2, 192, 33, 64)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 31 + M)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"gemv b{bits} M{M} K{K} N{N} g{gs}")
+
+
+def test_gemv_is_deterministic(ctx, oracle):
+    O = oracle
+    x, w_q, s, b, _ = O.make_problem(4, 4096, 512, 4, 64, F16, F16, seed=5)
+    y1 = run(ctx, x, w_q, s, b, 4, 4096, 512, 64, 4, F16, F16, F32, 1)
+    y2 = run(ctx, x, w_q, s, b, 4, 4096, 512, 64, 4, F16, F16, F32, 1)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+def test_generic_path_for_odd_k(ctx, oracle):
+    """K not a multiple of 64 (group 32) runs the generic kernel, which
+    accumulates in the oracle's order: bit-exact fp32."""
+    O = oracle
+    for K in (32, 96, 160):
+        x, w_q, s, b, _ = O.make_problem(3, K, 21, 3, 32, F32, F32, seed=K)
+        y = run(ctx, x, w_q, s, b, 3, K, 21, 32, 3, F32, F32, F32)
+        want = O.quantized_matmul(x, w_q, s, b, 3, K, 21, 32, 3, F32, F32, F32)
+        assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+# ---- full BASELINE shapes -----------------------------------------------
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_config1_decode_full(ctx, oracle, M):
+    """4-bit g64, K=4096, N=14336, fp16 x/scales/out."""
+    O = oracle
+    K, N = 4096, 14336
+    x, w_q, s, b, _ = O.make_problem(M, K, N, 4, 64, F16, F16, seed=1000 + M)
+    y = run(ctx, x, w_q, s, b, M, K, N, 64, 4, F16, F16, F16)
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, 64, 4, F16, F16, F16, variant="omp")
+    check_output(O, y, want, F16, f"config1 M={M}")
+
+
+def test_config0_cpu_plumbing_full(ctx, oracle):
+    """M=1, K=N=4096, 4-bit g64, fp32 everything: tolerance 1e-5."""
+    O = oracle
+    x, w_q, s, b, _ = O.make_problem(1, 4096, 4096, 4, 64, F32, F32, seed=0)
+    y = run(ctx, x, w_q, s, b, 1, 4096, 4096, 64, 4, F32, F32, F32)
+    want = O.quantized_matmul(x, w_q, s, b, 1, 4096, 4096, 64, 4, F32, F32, F32)
+    check_output(O, y, want, F32, "config0")
+
+
+@pytest.mark.parametrize("bits", [3, 6])
+@pytest.mark.parametrize("M", [1, 64])
+def test_config4_irregular_full(ctx, oracle, bits, M):
+    """3/6-bit g64, K=4096, N=11008, 1% x20 outliers, fp16."""
+    O = oracle
+    K, N = 4096, 11008
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, 64, F16, F16, seed=2000 + bits,
+                                     outlier_frac=0.01, outlier_scale=20.0)
+    # unpack is bit-exact: dequantized weights equal the oracle's
+    from mlx_amd import runtime
+    rows = slice(0, 256)
+    got = runtime.run_dequantize(ctx, w_q[rows], s[rows], b[rows], K, 64, bits, F16, F32)
+    assert np.array_equal(got, O.dequantize(w_q[rows], s[rows], b[rows], K, 64, bits, F16, F32))
+    y = run(ctx, x, w_q, s, b, M, K, N, 64, bits, F16, F16, F16)
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, 64, bits, F16, F16, F16, variant="omp")
+    check_output(O, y, want, F16, f"config4 b{bits} M{M}")
+
+
+def test_config2_crossover_full(ctx, oracle):
+    """8-bit g128, M=32, K=N=8192, bf16."""
+    O = oracle
+    M, K, N = 32, 8192, 8192
+    x, w_q, s, b, _ = O.make_problem(M, K, N, 8, 128, BF16, BF16, seed=3000)
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, variant="omp")
+    for kname, k in KERNELS.items():
+        y = run(ctx, x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, k)
+        check_output(O, y, want, BF16, f"config2 {kname}")
+
+
+# ---- errors -------------------------------------------------------------
+
+def test_error_codes(ctx, oracle):
+    from mlx_amd import abi, runtime
+    O = oracle
+    x, w_q, s, b, _ = O.make_problem(1, 256, 8, 4, 64, F16, F16, seed=1)
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    out = ctx.alloc(8 * 2)
+    q = ctx.q
+
+    def call(M=1, K=256, N=8, gs=64, bits=4, xd=F16, sbd=F16, od=F16, o=out):
+        return q.op_quantized_matmul(ctx.handle, *[t.handle for t in bufs], o.handle, M, K, N, gs,
+                                     bits, xd, sbd, od)
+    assert call() == abi.OK
+    assert call(bits=7) == abi.ERR_NOT_SUPPORTED
+    assert call(gs=48) == abi.ERR_NOT_SUPPORTED
+    assert call(xd=abi.INT32) == abi.ERR_NOT_SUPPORTED
+    assert call(K=250) == abi.ERR_INVALID_ARGUMENT       # K % group
+    assert call(N=9) == abi.ERR_INVALID_ARGUMENT         # buffers too small for the shape
+    assert call(M=-1) == abi.ERR_INVALID_ARGUMENT
+    assert call(M=0) == abi.OK and call(N=0) == abi.OK   # empty problems are no-ops
+    small = ctx.alloc(4)
+    assert call(o=small) == abi.ERR_INVALID_ARGUMENT
+    assert q.op_quantized_matmul_ex(ctx.handle, *[t.handle for t in bufs], out.handle, 1, 256, 8,
+                                    64, 4, F32, F16, F16, abi.KERNEL_GEMM) in (
+                                        abi.ERR_NOT_SUPPORTED, abi.ERR_INVALID_ARGUMENT)
+    ctx.sync()
+    for t in bufs + [out, small]:
+        t.free()
+    runtime._check(abi.OK, "ok")
