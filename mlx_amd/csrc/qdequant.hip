@@ -87,6 +87,7 @@ __global__ __launch_bounds__(256) void qmm_generic_kernel(const void* __restrict
                                                           void* __restrict__ y, int M, int K,
                                                           int N, int gsize, int bits, int x_dt,
                                                           int sb_dt, int out_dt) {
+#pragma clang fp contract(off)
     const size_t total = (size_t)M * N;
     const int G = K / gsize, rw = (K * bits) >> 5;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(256) void qmm_generic_kernel(const void* __restrict
             const size_t gi = (size_t)n * G + k / gsize;
             const float wv = fmaf(load_f(sc, gi, sb_dt), (float)row_code(row, k, bits),
                                   load_f(bi, gi, sb_dt));
-            acc = __fadd_rn(acc, __fmul_rn(load_f(x, (size_t)m * K + k, x_dt), wv));
+            acc = acc + load_f(x, (size_t)m * K + k, x_dt) * wv;
         }
         store_f(y, i, out_dt, acc);
     }

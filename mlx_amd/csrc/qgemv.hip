@@ -206,6 +206,7 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
     const int units = a.K / 64;
     const size_t lds = (size_t)MR * units * XL::kUnitStride * XL::kElem + (size_t)MR * (a.K / 32) * 4;
     if (lds > 64 * 1024) return LuxStatus::NotSupported;
+    (void)units;
     // rows per wave: enough waves to cover the chip several times over
     const int waves_wanted = 256 * 8;
     int rpw = (a.N + waves_wanted - 1) / waves_wanted;
@@ -245,12 +246,21 @@ LuxStatus launch_b(const QmmArgs& a, hipStream_t st) {
 
 }  // namespace
 
-// M is processed in chunks of at most 8 rows of x.
+size_t gemv_lds_bytes(int MR, int K, int x_dtype) {
+    const size_t elem = x_dtype == DT_F32 ? 4 : 2, stride = x_dtype == DT_F32 ? 68 : 72;
+    return (size_t)MR * (K / 64) * stride * elem + (size_t)MR * (K / 32) * 4;
+}
+
+// M is processed in chunks of up to 8 rows of x, as many as the staged x
+// fits in 64 KB of LDS (two blocks per CU).
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
-    for (int m0 = 0; m0 < args.M; m0 += 8) {
+    int chunk = 8;
+    while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
+    if (gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) return LuxStatus::NotSupported;
+    for (int m0 = 0; m0 < args.M; m0 += chunk) {
         QmmArgs a = args;
-        a.M = args.M - m0 < 8 ? args.M - m0 : 8;
+        a.M = args.M - m0 < chunk ? args.M - m0 : chunk;
         const size_t xel = args.x_dtype == DT_F32 ? 4 : 2, yel = args.out_dtype == DT_F32 ? 4 : 2;
         a.x = static_cast<const uint8_t*>(args.x) + (size_t)m0 * args.K * xel;
         a.y = static_cast<uint8_t*>(args.y) + (size_t)m0 * args.N * yel;

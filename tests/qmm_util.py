@@ -2,10 +2,13 @@
 construction.  The gates are the tolerances the north star states:
   fp32 output  max|d| / max|y| <= 1e-5
   fp16 output  max|d| / max|y| <= 1e-3
-  bf16 output  every element within one bf16 ulp of the oracle's bf16 value
-               (bf16 rounding of the output alone is ~2e-3 of max|y|, so the
+  bf16 output  every element within one bf16 ulp of the oracle's bf16 value,
+               plus 1e-5 * max|y| (the fp32 tolerance: near-zero outputs
+               have an ulp below fp32 accumulation-order differences).
+               bf16 rounding of the output alone is ~2e-3 of max|y|, so the
                1e-3 form cannot hold for any implementation; the literal
-               metric is still computed and returned)
+               metric is still computed and returned, and bf16 paths are
+               also checked with an fp32 output against the 1e-5 gate.
 """
 import numpy as np
 
@@ -35,7 +38,8 @@ def check_output(O, y_gpu, y_cpu, out_dtype, what=""):
     r = rel_err(g, c)
     if out_dtype == BF16:
         ulp = np.maximum(bf16_ulp(c), bf16_ulp(g))
-        bad = np.abs(g.astype(np.float64) - c.astype(np.float64)) > ulp * (1 + 1e-6)
+        floor = TOL[F32] * np.abs(c.astype(np.float64)).max()
+        bad = np.abs(g.astype(np.float64) - c.astype(np.float64)) > ulp * (1 + 1e-6) + floor
         assert not bad.any(), f"{what}: {bad.sum()} bf16 elements differ by more than 1 ulp (rel {r:.3g})"
     else:
         assert r <= TOL[out_dtype], f"{what}: max|d|/max|y| = {r:.3g} > {TOL[out_dtype]}"

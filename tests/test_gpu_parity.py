@@ -155,9 +155,14 @@ def test_config2_crossover_full(ctx, oracle):
     M, K, N = 32, 8192, 8192
     x, w_q, s, b, _ = O.make_problem(M, K, N, 8, 128, BF16, BF16, seed=3000)
     want = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, variant="omp")
+    want32 = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, F32, variant="omp")
     for kname, k in KERNELS.items():
         y = run(ctx, x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, k)
-        check_output(O, y, want, BF16, f"config2 {kname}")
+        r = check_output(O, y, want, BF16, f"config2 {kname}")
+        # the same kernel with an fp32 epilogue meets the fp32 gate
+        y32 = run(ctx, x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, F32, k)
+        r32 = check_output(O, y32, want32, F32, f"config2 {kname} fp32 out")
+        print(f"config2 {kname}: bf16-out max|d|/max|y| = {r:.3g}, fp32-out = {r32:.3g}")
 
 
 # ---- errors -------------------------------------------------------------
