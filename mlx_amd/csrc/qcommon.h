@@ -88,30 +88,74 @@ __device__ __host__ __forceinline__ int x_slot(int k) {
     }
 }
 
+// gfx9 VOP3 encodings take no literal constants and read at most one SGPR,
+// so the compiler splits (x & mask) | magic into v_and + v_or.  These emit
+// the fused forms with the mask in an SGPR and the magic in a VGPR.
+__device__ __forceinline__ uint32_t vconst(uint32_t c) {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(c));
+    return v;
+}
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t vmagic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(vmagic));
+    return r;
+}
+template <int S>
+__device__ __forceinline__ uint32_t lshl_or(uint32_t x, uint32_t vmagic) {
+    uint32_t r;
+    asm("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "i"(S), "v"(vmagic));
+    return r;
+}
+
+// Where the operand builder places a code inside each 16-bit half, and the
+// factor that maps sum x v(q) back to sum x q.  For BITS 2/4/8 the code LSB
+// goes to P, the highest multiple of BITS that leaves the code inside the
+// mantissa: one code per word then needs no shift, and v(q) = 1 + q 2^(P-MANT).
+// Irregular widths place the code at the top of the mantissa.
+template <int BITS, int MANT>
+struct MagicCfg {
+    static constexpr bool kApart = PairLayout<BITS>::kApart;
+    static constexpr int P = kApart ? ((MANT - BITS) / BITS) * BITS : MANT - BITS;
+    static constexpr float kPow = (float)(1u << (MANT - P));  // v(q) = 1 + q / kPow
+};
+
 // Build the 32 operand pairs of one 64-code unit.  MANT = 10 (f16) or 7 (bf16).
 template <int BITS, int MANT>
 __device__ __forceinline__ void unit_pairs_magic(const uint32_t* w, uint32_t* pr) {
+    using C = MagicCfg<BITS, MANT>;
     constexpr uint32_t one = (MANT == 10) ? 0x3C00u : 0x3F80u;
-    constexpr uint32_t magic = one | (one << 16);
-    constexpr uint32_t m16 = ((1u << BITS) - 1u) << (MANT - BITS);
-    constexpr uint32_t mask = m16 | (m16 << 16);
-    if constexpr (PairLayout<BITS>::kApart) {
-        constexpr int P = PairLayout<BITS>::kCodesPerWord, H = P / 2;
+    const uint32_t magic = vconst(one | (one << 16));
+    if constexpr (C::kApart) {
+        constexpr int H = PairLayout<BITS>::kCodesPerWord / 2;
+        constexpr uint32_t m16 = ((1u << BITS) - 1u) << C::P;
+        constexpr uint32_t mask = m16 | (m16 << 16);
 #pragma unroll
         for (int wi = 0; wi < 2 * BITS; wi++) {
 #pragma unroll
             for (int j = 0; j < H; j++) {
-                // low code at bit j*BITS -> bit MANT-BITS
-                const int s = (MANT - BITS) - j * BITS;
-                uint32_t v = s >= 0 ? (w[wi] << s) : (w[wi] >> (-s));
-                pr[wi * H + j] = (v & mask) | magic;
+                // code j of the low half sits at bit j*BITS; move it to P
+                const int s = C::P - j * BITS;
+                uint32_t r;
+                if (s == 0) {
+                    r = and_or(w[wi], mask, magic);
+                } else if (s > 0) {
+                    // mask first, then shift into place and OR the magic
+                    r = (w[wi] & (mask >> s));
+                    r = (s == 1) ? lshl_or<1>(r, magic) : (s == 2) ? lshl_or<2>(r, magic)
+                      : (s == 4) ? lshl_or<4>(r, magic) : (s == 6) ? lshl_or<6>(r, magic)
+                      : lshl_or<8>(r, magic);
+                } else {
+                    r = and_or(w[wi] >> (-s), mask, magic);
+                }
+                pr[wi * H + j] = r;
             }
         }
     } else {
 #pragma unroll
         for (int p = 0; p < 32; p++) {
             uint32_t lo = unit_code<BITS>(w, 2 * p), hi = unit_code<BITS>(w, 2 * p + 1);
-            pr[p] = ((lo | (hi << 16)) << (MANT - BITS)) | magic;
+            pr[p] = lshl_or<MANT - BITS>(lo | (hi << 16), magic);
         }
     }
 }

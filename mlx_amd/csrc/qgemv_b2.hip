@@ -1,0 +1,8 @@
+// qgemv_b2.hip -- 2-bit instantiations of the GEMV kernels.
+#include "qgemv_impl.h"
+
+namespace lxq {
+namespace gemv {
+template LuxStatus launch_b<2>(const QmmArgs&, hipStream_t);
+}  // namespace gemv
+}  // namespace lxq

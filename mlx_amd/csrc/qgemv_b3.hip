@@ -1,0 +1,8 @@
+// qgemv_b3.hip -- 3-bit instantiations of the GEMV kernels.
+#include "qgemv_impl.h"
+
+namespace lxq {
+namespace gemv {
+template LuxStatus launch_b<3>(const QmmArgs&, hipStream_t);
+}  // namespace gemv
+}  // namespace lxq

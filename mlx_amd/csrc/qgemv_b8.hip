@@ -1,0 +1,8 @@
+// qgemv_b8.hip -- 8-bit instantiations of the GEMV kernels.
+#include "qgemv_impl.h"
+
+namespace lxq {
+namespace gemv {
+template LuxStatus launch_b<8>(const QmmArgs&, hipStream_t);
+}  // namespace gemv
+}  // namespace lxq

@@ -283,7 +283,16 @@ int lux_cpu_quantized_matmul(void* y, const void* x, const uint32_t* w_q,
                              const void* scales, const void* biases,
                              int M, int K, int N, int group_size, int bits,
                              int x_dtype, int sb_dtype, int out_dtype) {
+    return lux_cpu_quantized_matmul_wround(y, x, w_q, scales, biases, M, K, N, group_size, bits,
+                                           x_dtype, sb_dtype, out_dtype, LUX_CPU_F32);
+}
+
+int lux_cpu_quantized_matmul_wround(void* y, const void* x, const uint32_t* w_q,
+                                    const void* scales, const void* biases,
+                                    int M, int K, int N, int group_size, int bits,
+                                    int x_dtype, int sb_dtype, int out_dtype, int w_dtype) {
     int rc = lux_cpu_quant_check(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype);
+    if (!rc && !dtype_ok(w_dtype)) rc = LUX_CPU_ENOTSUP;
     if (rc) return rc;
     if ((M && N) && (!y || !x || !w_q || !scales || !biases)) return LUX_CPU_EINVAL;
     const int wpr = K * bits / 32;
@@ -293,6 +302,11 @@ int lux_cpu_quantized_matmul(void* y, const void* x, const uint32_t* w_q,
     for (size_t i = 0; i < (size_t)M * K; i++) xf[i] = load_el(x, i, x_dtype);
     for (int n = 0; n < N; n++) {
         dequant_row_f32(wrow, w_q + (size_t)n * wpr, scales, biases, n, K, group_size, bits, sb_dtype);
+        if (w_dtype != LUX_CPU_F32)
+            for (int k = 0; k < K; k++) {
+                uint16_t h = w_dtype == LUX_CPU_F16 ? lux_cpu_f32_to_f16(wrow[k]) : lux_cpu_f32_to_bf16(wrow[k]);
+                wrow[k] = w_dtype == LUX_CPU_F16 ? lux_cpu_f16_to_f32(h) : lux_cpu_bf16_to_f32(h);
+            }
         for (int m = 0; m < M; m++) {
             const float* xr = xf + (size_t)m * K;
             float sum = 0.0f;

@@ -89,6 +89,23 @@ int lux_cpu_quantized_matmul_omp(void* y, const void* x, const uint32_t* w_q,
                                  int x_dtype, int sb_dtype, int out_dtype,
                                  int num_threads);
 
+/* lux_cpu_quantized_matmul_wround: the same scalar oracle with the
+ *   dequantized weight rounded (RNE) to w_dtype before the multiply:
+ *   y = sum_k x_k * T(fmaf(s, q, b)).  w_dtype F32 is the exact form above;
+ *   F16/BF16 is the "dequantize to the activation type, then matmul"
+ *   semantics of a GEMM that stages dequantized tiles for 16-bit MFMA.    */
+int lux_cpu_quantized_matmul_wround(void* y, const void* x, const uint32_t* w_q,
+                                    const void* scales, const void* biases,
+                                    int M, int K, int N, int group_size, int bits,
+                                    int x_dtype, int sb_dtype, int out_dtype,
+                                    int w_dtype);
+
+int lux_cpu_quantized_matmul_wround_omp(void* y, const void* x, const uint32_t* w_q,
+                                        const void* scales, const void* biases,
+                                        int M, int K, int N, int group_size, int bits,
+                                        int x_dtype, int sb_dtype, int out_dtype, int w_dtype,
+                                        int num_threads);
+
 /* argument validation shared by all entry points: returns LUX_CPU_OK,
  * LUX_CPU_EINVAL (bad shape) or LUX_CPU_ENOTSUP (unsupported bits/group/dtype) */
 int lux_cpu_quant_check(int M, int K, int N, int group_size, int bits,

@@ -12,6 +12,7 @@
  */
 #include "lux_cpu_quant.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -104,5 +105,56 @@ int lux_cpu_quantized_matmul_omp(void* y, const void* x, const uint32_t* w_q,
     }
     free(xf);
     free(xs);
+    return LUX_CPU_OK;
+}
+
+/* OpenMP form of lux_cpu_quantized_matmul_wround (rows of W in parallel,
+ * dequantized row rounded to w_dtype, fp32 accumulation): the checker for
+ * large GEMM shapes.  Same values as the scalar form up to fp32 summation
+ * order. */
+int lux_cpu_quantized_matmul_wround_omp(void* y, const void* x, const uint32_t* w_q,
+                                        const void* scales, const void* biases,
+                                        int M, int K, int N, int group_size, int bits,
+                                        int x_dtype, int sb_dtype, int out_dtype, int w_dtype,
+                                        int num_threads) {
+    int rc = lux_cpu_quant_check(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return LUX_CPU_OK;
+    const int G = K / group_size, wpr = K * bits / 32;
+    float* xf = (float*)malloc((size_t)M * K * sizeof(float));
+    if (!xf) return LUX_CPU_EINVAL;
+    for (size_t i = 0; i < (size_t)M * K; i++) xf[i] = ld(x, i, x_dtype);
+#ifdef _OPENMP
+    if (num_threads > 0) omp_set_num_threads(num_threads);
+#pragma omp parallel
+#endif
+    {
+        float* q = (float*)malloc((size_t)K * sizeof(float));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int n = 0; n < N; n++) {
+            unpack_row(q, w_q + (size_t)n * wpr, K, bits);
+            for (int k = 0; k < K; k++) {
+                const int g = k / group_size;
+                float v = fmaf(ld(scales, (size_t)n * G + g, sb_dtype), q[k],
+                               ld(biases, (size_t)n * G + g, sb_dtype));
+                if (w_dtype == LUX_CPU_F16) v = lux_cpu_f16_to_f32(lux_cpu_f32_to_f16(v));
+                else if (w_dtype == LUX_CPU_BF16) v = lux_cpu_bf16_to_f32(lux_cpu_f32_to_bf16(v));
+                q[k] = v;
+            }
+            for (int m = 0; m < M; m++) {
+                const float* xr = xf + (size_t)m * K;
+                float acc = 0.f;
+#ifdef _OPENMP
+#pragma omp simd reduction(+ : acc)
+#endif
+                for (int k = 0; k < K; k++) acc += xr[k] * q[k];
+                st(y, (size_t)m * N + n, out_dtype, acc);
+            }
+        }
+        free(q);
+    }
+    free(xf);
     return LUX_CPU_OK;
 }

@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
         L.lux_cpu_quantized_matmul.argtypes = [P, P, P, P, P] + [I] * 8
         L.lux_cpu_quantized_matmul_f64.argtypes = [P, P, P, P, P] + [I] * 7
         L.lux_cpu_quantized_matmul_omp.argtypes = [P, P, P, P, P] + [I] * 9
+        L.lux_cpu_quantized_matmul_wround.argtypes = [P, P, P, P, P] + [I] * 9
+        L.lux_cpu_quantized_matmul_wround_omp.argtypes = [P, P, P, P, P] + [I] * 10
         L.lux_cpu_quant_check.argtypes = [I] * 8
         _lib = L
     return _lib
@@ -146,11 +148,14 @@ def dequantize(w_q, scales, biases, K: int, group_size: int, bits: int,
 
 def quantized_matmul(x, w_q, scales, biases, M: int, K: int, N: int, group_size: int,
                      bits: int, x_dtype: int, sb_dtype: int, out_dtype: int,
-                     variant: str = "ref", threads: int = 0) -> np.ndarray:
+                     variant: str = "ref", threads: int = 0, w_round: int = F32) -> np.ndarray:
     """y[M, N] = x[M, K] . dequant(W)[N, K]^T.
 
     variant "ref": scalar oracle;  "f64": fp64 accumulation (returns float64);
     "omp": the timed OpenMP baseline.
+    w_round F16/BF16: the dequantized weight is rounded to that type before
+    the multiply (the GEMM's "dequantize to the activation type" semantics);
+    with variant "ref" the scalar oracle, with "omp" its OpenMP form.
     """
     args = [np.ascontiguousarray(a) for a in (x, w_q, scales, biases)]
     L = lib()
@@ -160,6 +165,18 @@ def quantized_matmul(x, w_q, scales, biases, M: int, K: int, N: int, group_size:
                                               group_size, bits, x_dtype, sb_dtype), "matmul_f64")
         return y
     y = np.empty((M, N), dtype=_NP[out_dtype])
+    if w_round != F32:
+        if variant == "ref":
+            rc = L.lux_cpu_quantized_matmul_wround(_p(y), *[_p(a) for a in args], M, K, N, group_size,
+                                                   bits, x_dtype, sb_dtype, out_dtype, w_round)
+        elif variant == "omp":
+            rc = L.lux_cpu_quantized_matmul_wround_omp(_p(y), *[_p(a) for a in args], M, K, N,
+                                                       group_size, bits, x_dtype, sb_dtype, out_dtype,
+                                                       w_round, threads)
+        else:
+            raise ValueError(variant)
+        _check(rc, "quantized_matmul_wround")
+        return y
     if variant == "ref":
         rc = L.lux_cpu_quantized_matmul(_p(y), *[_p(a) for a in args], M, K, N, group_size,
                                         bits, x_dtype, sb_dtype, out_dtype)

@@ -144,9 +144,16 @@ def test_config4_irregular_full(ctx, oracle, bits, M):
     rows = slice(0, 256)
     got = runtime.run_dequantize(ctx, w_q[rows], s[rows], b[rows], K, 64, bits, F16, F32)
     assert np.array_equal(got, O.dequantize(w_q[rows], s[rows], b[rows], K, 64, bits, F16, F32))
+    from mlx_amd import abi
+    gemm = ctx.select_kernel(M, K, N, 64, bits, F16) == abi.KERNEL_GEMM
     y = run(ctx, x, w_q, s, b, M, K, N, 64, bits, F16, F16, F16)
-    want = O.quantized_matmul(x, w_q, s, b, M, K, N, 64, bits, F16, F16, F16, variant="omp")
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, 64, bits, F16, F16, F16, variant="omp",
+                              w_round=F16 if gemm else F32)
     check_output(O, y, want, F16, f"config4 b{bits} M{M}")
+    if gemm:
+        # f16 weight rounding stays inside the f16 gate against the exact form too
+        exact = O.quantized_matmul(x, w_q, s, b, M, K, N, 64, bits, F16, F16, F16, variant="omp")
+        check_output(O, y, exact, F16, f"config4 b{bits} M{M} vs exact")
 
 
 def test_config2_crossover_full(ctx, oracle):
@@ -156,12 +163,21 @@ def test_config2_crossover_full(ctx, oracle):
     x, w_q, s, b, _ = O.make_problem(M, K, N, 8, 128, BF16, BF16, seed=3000)
     want = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, variant="omp")
     want32 = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, F32, variant="omp")
+    wantT = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, variant="omp",
+                               w_round=BF16)
+    wantT32 = O.quantized_matmul(x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, F32, variant="omp",
+                                 w_round=BF16)
+    from mlx_amd import abi
+    sel = ctx.select_kernel(M, K, N, 128, 8, BF16)
     for kname, k in KERNELS.items():
+        # the GEMM (and AUTO when it picks the GEMM) dequantizes to bf16 first
+        gemm = k == abi.KERNEL_GEMM or (k == abi.KERNEL_AUTO and sel == abi.KERNEL_GEMM)
+        ref, ref32 = (wantT, wantT32) if gemm else (want, want32)
         y = run(ctx, x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, BF16, k)
-        r = check_output(O, y, want, BF16, f"config2 {kname}")
+        r = check_output(O, y, ref, BF16, f"config2 {kname}")
         # the same kernel with an fp32 epilogue meets the fp32 gate
         y32 = run(ctx, x, w_q, s, b, M, K, N, 128, 8, BF16, BF16, F32, k)
-        r32 = check_output(O, y32, want32, F32, f"config2 {kname} fp32 out")
+        r32 = check_output(O, y32, ref32, F32, f"config2 {kname} fp32 out")
         print(f"config2 {kname}: bf16-out max|d|/max|y| = {r:.3g}, fp32-out = {r32:.3g}")
 
 
@@ -195,3 +211,47 @@ def test_error_codes(ctx, oracle):
     for t in bufs + [out, small]:
         t.free()
     runtime._check(abi.OK, "ok")
+
+
+# ---- GEMM (dequantize to the activation type, MFMA) ----------------------
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("xd,sbd,od", [(BF16, BF16, BF16), (F16, F16, F16), (BF16, F32, F32),
+                                       (F16, BF16, F32)])
+def test_gemm_parity(ctx, oracle, bits, xd, sbd, od):
+    """The GEMM equals the oracle's "dequantize to T, then matmul" form
+    (w_round = x dtype) to the dtype gates; ragged M and N exercise the
+    tile edges."""
+    O = oracle
+    for (M, K, N, gs) in [(300, 512, 200, 64), (256, 1024, 128, 32), (33, 256, 130, 128),
+                          (512, 128, 384, 64)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 17 + M)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, w_round=xd)
+        check_output(O, y, want, od, f"gemm b{bits} M{M} K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("N", [4096, 14336])
+def test_config3_prefill_sampled(ctx, oracle, N):
+    """M=2048, K=4096, 4-bit g64, bf16.  The whole output is
+    computed on the GPU; 96 seeded rows of it are checked against the oracle
+    (the dequantize-to-bf16 form, bf16 and fp32 outputs), and the deviation
+    from the exact fp32-weight form is reported."""
+    O = oracle
+    M, K = 2048, 4096
+    x, w_q, s, b, _ = O.make_problem(M, K, N, 4, 64, BF16, BF16, seed=4000 + N)
+    rows = np.sort(np.random.default_rng(N).choice(M, 96, replace=False))
+    xs = np.ascontiguousarray(x[rows])
+    for od in (BF16, F32):
+        y = run(ctx, x, w_q, s, b, M, K, N, 64, 4, BF16, BF16, od)
+        ys = np.ascontiguousarray(y[rows])
+        want = O.quantized_matmul(xs, w_q, s, b, len(rows), K, N, 64, 4, BF16, BF16, od,
+                                  variant="omp", w_round=BF16)
+        r = check_output(O, ys, want, od, f"config3 N={N} out={od}")
+        exact = O.quantized_matmul(xs, w_q, s, b, len(rows), K, N, 64, 4, BF16, BF16, F32,
+                                   variant="omp")
+        g = O.to_f32(ys, od) if od != F32 else ys
+        dev = float(np.abs(g - exact).max() / np.abs(exact).max())
+        print(f"config3 N={N} out={od}: vs dequant-to-bf16 oracle {r:.3g}, vs exact-weight oracle {dev:.3g}")
+        # bf16 weight rounding (2^-9 relative per weight) bounds the deviation
+        assert dev < 8e-3
