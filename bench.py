@@ -79,6 +79,29 @@ class Hip:
     def sync(self, stream):
         self.ck(self.L.hipStreamSynchronize(ctypes.c_void_p(stream)), "hipStreamSynchronize")
 
+    def malloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self.ck(self.L.hipMalloc(ctypes.byref(p), ctypes.c_size_t(nbytes)), "hipMalloc")
+        return p
+
+    def free(self, p):
+        self.ck(self.L.hipFree(p), "hipFree")
+
+
+def calibrate_copy(hip, nbytes, reps=8):
+    """A plain device-to-device copy of nbytes (ROCm runs it as a blit
+    kernel), the known-size reference that scales the FETCH_SIZE/WRITE_SIZE
+    counters of the profiled kernels to bytes."""
+    src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+    hip.ck(hip.L.hipMemset(src, 0x5A, ctypes.c_size_t(nbytes)), "hipMemset")
+    hip.ck(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    for _ in range(reps):
+        hip.ck(hip.L.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3), "hipMemcpy D2D")
+    hip.ck(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    hip.free(src)
+    hip.free(dst)
+    print(json.dumps({"calibrate_copy_bytes": nbytes, "reps": reps}), flush=True)
+
 
 def make_weights(ctx, N, K, bits, gs, sb, copies, seed):
     """W ~ N(0, 0.02) on the host, quantized on the GPU by the plugin's
@@ -187,6 +210,24 @@ def cpu_baseline(M, K, N, bits, gs, budget_s=10.0):
                       f"{bits}-bit g{gs} f16, {el:.1f} s"}
 
 
+GEMV_PROFILE = os.path.join(ROOT, "profiles", "qgemv_m1_k4096_n14336_4bit_g64_f16.md")
+
+
+def profiled_traffic(path):
+    """HBM bytes per launch of the headline kernel: FETCH_SIZE + WRITE_SIZE
+    from two rocprofv3 --pmc runs of this script, each scaled by the same
+    counter's reading for a plain copy of known size (the summary under
+    profiles/ gives the commands and the factors).  None when absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,7 +235,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run a device-to-device copy of BYTES (counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy(Hip(), args.calibrate_copy)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the plugin path is single-device; see DESIGN.md for how it would shard)",
@@ -228,7 +274,8 @@ def main():
         "config": {"workload": "configs[1] decode GEMV M=1", "M": M, "K": K, "N": N, "bits": bits,
                    "group_size": gs, "kernel": "gemv", "hbm_pct": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(GEMV_PROFILE),
                      "kernel": "qgemv_reg_kernel", "kernel_us_avg": round(r["kernel_ms_avg"] * 1e3, 3),
                      "kernel_us_single_launch": round(r["single_ms_avg"] * 1e3, 3),
                      "algorithmic_bytes": wb},
