@@ -14,7 +14,9 @@ oracle function is pinned by checks that a plausible mistake fails:
     exact integer matmul (scale 1, bias 0), and bit for bit against the
     reference CPU backend's op_matmul_f32 (reference src/cpu_backend.cpp:
     243-266, compiled from its source into oracle/_ref) applied to the
-    dequantized weights.
+    dequantized weights;
+  * the dequantize-to-T form (w_round) bit for bit against the same
+    reference op on T-rounded weights, and its OpenMP form against fp64.
 """
 import ctypes
 import hashlib
@@ -302,6 +304,30 @@ def test_bit_exact_vs_reference_cpu_backend(oracle, bits):
     c = ref_dense_matmul(desc, np.ascontiguousarray(x), np.ascontiguousarray(what.T))
     y = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, O.F32, O.F32, O.F32)
     assert np.array_equal(y.view(np.uint32), c.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [3, 4, 8])
+@pytest.mark.parametrize("wt", [1, 2])
+def test_wround_bit_exact_vs_reference_cpu_backend(oracle, bits, wt):
+    """The dequantize-to-T form (the GEMM's semantics) equals the reference
+    CPU backend's op_matmul_f32 applied to the dequantized weights rounded to
+    T (f16 / bf16) and widened back, bit for bit; the OpenMP form of it stays
+    within fp32 accumulation error of the fp64 product of the same operands."""
+    O = oracle
+    _, desc = _ref_cpu_backend()
+    M, K, N, gs = 5, 512, 36, 64
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, wt, wt, seed=13 + bits)
+    what_t = O.to_f32(O.dequantize(w_q, s, b, K, gs, bits, wt, out_dtype=wt), wt)
+    # the rounding is visible: the T-rounded weights differ from the fp32 ones
+    assert not np.array_equal(what_t, O.dequantize(w_q, s, b, K, gs, bits, wt))
+    xf = np.ascontiguousarray(O.to_f32(x, wt))
+    c = ref_dense_matmul(desc, xf, np.ascontiguousarray(what_t.T))
+    y = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, wt, wt, O.F32, w_round=wt)
+    assert np.array_equal(y.view(np.uint32), c.view(np.uint32))
+    exact = xf.astype(np.float64) @ what_t.astype(np.float64).T
+    yo = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, wt, wt, O.F32, variant="omp",
+                            threads=2, w_round=wt)
+    assert np.abs(yo - exact).max() <= 1e-5 * np.abs(exact).max()
 
 
 def test_check_args(oracle):
