@@ -263,11 +263,18 @@ int gemv_max_m() {
     return v;
 }
 
+// shapes the MFMA GEMM takes: 16-bit activations, K a multiple of 256 (its
+// scale windows span 4 K steps of 64), x and W below 4 GiB (32-bit offsets)
+bool gemm_ok(int M, int K, int N, int bits, LuxBackendDtype x_dtype) {
+    return x_dtype != LUX_DTYPE_FLOAT32 && K % 256 == 0 &&
+           (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
+}
+
 LuxQuantKernel select_kernel_impl(int M, int K, int N, int group_size, int bits,
                                   LuxBackendDtype x_dtype) {
-    (void)N; (void)group_size; (void)bits;
-    if (x_dtype == LUX_DTYPE_FLOAT32 || K % 64 != 0) return LUX_QMM_KERNEL_GEMV;
-    return M <= gemv_max_m() ? LUX_QMM_KERNEL_GEMV : LUX_QMM_KERNEL_GEMM;
+    (void)group_size;
+    if (M <= gemv_max_m() || !gemm_ok(M, K, N, bits, x_dtype)) return LUX_QMM_KERNEL_GEMV;
+    return LUX_QMM_KERNEL_GEMM;
 }
 
 LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBuffer* w_q,
@@ -304,12 +311,10 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
     if (kernel == LUX_QMM_KERNEL_AUTO) kernel = select_kernel_impl(M, K, N, group_size, bits, x_dtype);
     if (kernel == LUX_QMM_KERNEL_GEMM) {
-        if (x_dtype == LUX_DTYPE_FLOAT32) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
-        if (K % 64 == 0) {
-            lxq::LuxStatus s = lxq::launch_qgemm(a, ctx->stream);
-            if (s != lxq::LuxStatus::NotSupported) return map_status(s);
-        }
-        // shapes the GEMM tiling cannot take fall through to the GEMV
+        // an explicit GEMM request runs the GEMM or fails: its numerics
+        // (weights rounded to the activation type) differ from the GEMV's
+        if (!gemm_ok(M, K, N, bits, x_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+        return map_status(lxq::launch_qgemm(a, ctx->stream));
     }
     if (K % 64 == 0) {
         lxq::LuxStatus s = lxq::launch_qgemv(a, ctx->stream);

@@ -224,11 +224,34 @@ def test_gemm_parity(ctx, oracle, bits, xd, sbd, od):
     tile edges."""
     O = oracle
     for (M, K, N, gs) in [(300, 512, 200, 64), (256, 1024, 128, 32), (33, 256, 130, 128),
-                          (512, 128, 384, 64)]:
+                          (512, 768, 384, 64)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 17 + M)
         y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, w_round=xd)
         check_output(O, y, want, od, f"gemm b{bits} M{M} K{K} N{N} g{gs}")
+
+
+def test_gemm_shape_limits(ctx, oracle):
+    """K not a multiple of 256: an explicit GEMM request is NOT_SUPPORTED,
+    AUTO picks the GEMV (exact weights) for any M."""
+    from mlx_amd import abi
+    O = oracle
+    M, K, N = 64, 192, 40
+    assert ctx.select_kernel(M, K, N, 64, 4, F16) == abi.KERNEL_GEMV
+    assert ctx.select_kernel(M, 256, N, 64, 4, F16) == abi.KERNEL_GEMM
+    assert ctx.select_kernel(M, 256, N, 64, 4, F32) == abi.KERNEL_GEMV
+    x, w_q, s, b, _ = O.make_problem(M, K, N, 4, 64, F16, F16, seed=5)
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    out = ctx.alloc(M * N * 4)
+    rc = ctx.q.op_quantized_matmul_ex(ctx.handle, *[t.handle for t in bufs], out.handle, M, K, N,
+                                      64, 4, F16, F16, F32, abi.KERNEL_GEMM)
+    assert rc == abi.ERR_NOT_SUPPORTED
+    ctx.sync()
+    for t in bufs + [out]:
+        t.free()
+    y = run(ctx, x, w_q, s, b, M, K, N, 64, 4, F16, F16, F32)
+    check_output(O, y, O.quantized_matmul(x, w_q, s, b, M, K, N, 64, 4, F16, F16, F32), F32,
+                 "auto K=192")
 
 
 @pytest.mark.parametrize("N", [4096, 14336])
