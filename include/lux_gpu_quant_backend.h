@@ -86,9 +86,9 @@ typedef struct lux_gpu_quant_vtbl {
     /* the context's hipStream_t, for callers that time or order work on it */
     void* (*get_native_stream)(LuxBackendContext* ctx);
 
-    /* which kernel AUTO picks for this shape (no launch) */
+    /* which kernel AUTO picks for this shape and these dtypes (no launch) */
     LuxQuantKernel (*select_kernel)(int M, int K, int N, int group_size, int bits,
-                                    LuxBackendDtype x_dtype);
+                                    LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype);
 
     void* _reserved[8];
 } lux_gpu_quant_vtbl;

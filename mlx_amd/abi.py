@@ -125,7 +125,7 @@ OP_QMM_EX = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, Buf, Buf, _I, _I, _I, _I, _I, _
 OP_DEQUANT = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, Buf, _I, _I, _I, _I, _I, _I)
 OP_QUANT = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, Buf, _I, _I, _I, _I, _I, _I)
 GET_NATIVE_STREAM = C.CFUNCTYPE(C.c_void_p, Ctx)
-SELECT_KERNEL = C.CFUNCTYPE(_I, _I, _I, _I, _I, _I, _I)
+SELECT_KERNEL = C.CFUNCTYPE(_I, _I, _I, _I, _I, _I, _I, _I)
 
 
 class QuantVtbl(C.Structure):

@@ -264,16 +264,20 @@ int gemv_max_m() {
 }
 
 // shapes the MFMA GEMM takes: 16-bit activations, K a multiple of 256 (its
-// scale windows span 4 K steps of 64), x and W below 4 GiB (32-bit offsets)
-bool gemm_ok(int M, int K, int N, int bits, LuxBackendDtype x_dtype) {
+// scale windows span 4 K steps of 64), x and W below 4 GiB (32-bit offsets),
+// and its LDS buffers within one CU's 160 KB (f32 scales at group size 32
+// with 6- or 8-bit codes do not fit)
+bool gemm_ok(int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dtype,
+             LuxBackendDtype sb_dtype) {
+    if (sb_dtype == LUX_DTYPE_FLOAT32 && group_size == 32 && bits >= 6) return false;
     return x_dtype != LUX_DTYPE_FLOAT32 && K % 256 == 0 &&
            (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
 }
 
 LuxQuantKernel select_kernel_impl(int M, int K, int N, int group_size, int bits,
-                                  LuxBackendDtype x_dtype) {
-    (void)group_size;
-    if (M <= gemv_max_m() || !gemm_ok(M, K, N, bits, x_dtype)) return LUX_QMM_KERNEL_GEMV;
+                                  LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype) {
+    if (M <= gemv_max_m() || !gemm_ok(M, K, N, group_size, bits, x_dtype, sb_dtype))
+        return LUX_QMM_KERNEL_GEMV;
     return LUX_QMM_KERNEL_GEMM;
 }
 
@@ -309,11 +313,12 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     a.x_dtype = x_dtype; a.sb_dtype = sb_dtype; a.out_dtype = out_dtype;
 
     if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
-    if (kernel == LUX_QMM_KERNEL_AUTO) kernel = select_kernel_impl(M, K, N, group_size, bits, x_dtype);
+    if (kernel == LUX_QMM_KERNEL_AUTO)
+        kernel = select_kernel_impl(M, K, N, group_size, bits, x_dtype, sb_dtype);
     if (kernel == LUX_QMM_KERNEL_GEMM) {
         // an explicit GEMM request runs the GEMM or fails: its numerics
         // (weights rounded to the activation type) differ from the GEMV's
-        if (!gemm_ok(M, K, N, bits, x_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+        if (!gemm_ok(M, K, N, group_size, bits, x_dtype, sb_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
         return map_status(lxq::launch_qgemm(a, ctx->stream));
     }
     if (K % 64 == 0) {
@@ -391,8 +396,8 @@ void* hip_get_native_stream(LuxBackendContext* c) {
 }
 
 LuxQuantKernel hip_select_kernel(int M, int K, int N, int group_size, int bits,
-                                 LuxBackendDtype x_dtype) {
-    return select_kernel_impl(M, K, N, group_size, bits, x_dtype);
+                                 LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype) {
+    return select_kernel_impl(M, K, N, group_size, bits, x_dtype, sb_dtype);
 }
 
 // ---------------------------------------------------------------------------

@@ -54,8 +54,9 @@ __device__ __forceinline__ uint32_t unit_code(const uint32_t* w, int i) {
     const int bit = i * BITS, wi = bit >> 5, sh = bit & 31;
     const uint32_t mask = (1u << BITS) - 1u;
     if (sh + BITS <= 32) return (w[wi] >> sh) & mask;
-    uint64_t pair = ((uint64_t)w[wi + 1] << 32) | w[wi];
-    return (uint32_t)(pair >> sh) & mask;
+    // straddling code: funnel shift (a 64-bit shift can push the word array
+    // into a private-memory copy)
+    return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & mask;
 }
 
 // Exact 16-bit operand pairs for the dot2 instructions.

@@ -7,25 +7,30 @@
 // "dequantize to the activation type, then matmul" semantics.
 //
 // Block tile 256 (M) x 128 (N), 8 waves (two per SIMD) as 4 x 2, wave tile
-// 64 x 64 = 2 x 2 MFMA tiles of 32 x 32.  Waves 0..3 (one per SIMD) also
-// load and dequantize W; waves 4..7 only load x and run MFMAs.  The two
-// roles are separate compile-time code paths, so each keeps a fixed number
-// of loads in flight and its waits are constants.
+// 64 x 64 = 2 x 2 MFMA tiles of 32 x 32.  Every wave also dequantizes 16
+// codes of one W row per K step.
 //
-// LDS: three x stages (256 rows x 64 k, 32 KB each, filled straight from
-// global memory by global_load_lds_dwordx4) and two dequantized W stages
-// (128 rows x 64 k, 16 KB each).  Rows are 128 B; 16-byte chunk c of row r
-// sits at position c ^ swz(r), which makes the fragment reads (16 lanes =
-// 16 consecutive rows, one chunk), the dequant writes (same shape) and the
-// direct x writes (contiguous) free of bank conflicts for 8- and 16-lane
-// LDS passes alike.
+// All operands reach LDS by direct global->LDS transfers (global_load_lds):
+// x tiles (all waves), packed W (waves 0..3) and scale/bias windows (waves
+// 4..7).  No vector-memory load lands in registers inside the K loop, so the
+// compiler adds no waits of its own and the explicit per-step waits count
+// every transfer in flight; the two wave roles are separate compile-time
+// code paths with their own constant waits.
 //
-// Pipeline: x runs two K steps ahead; packed W runs four steps ahead in
-// registers; scales and biases are loaded once per 4 K steps as one aligned
-// window per row (GS = group size is a template parameter so the window is
-// a compile-time shape; K must be a multiple of 256).  While the MFMAs of
-// step k run, step k+1 is dequantized into the other W stage in two halves
-// between them: one barrier per K step.
+// LDS: three x stages (256 rows x 64 k, 32 KB each), two dequantized W
+// stages (128 rows x 64 k, 16 KB each), three packed W slots (one K step
+// each) and two scale windows (4 K steps each).  x and dequantized-W rows
+// are 128 B; 16-byte chunk c of row r sits at position c ^ swz(r), which
+// makes the fragment reads (16 lanes = 16 consecutive rows, one chunk), the
+// dequant writes (same shape) and the direct x writes (contiguous) free of
+// bank conflicts for 8- and 16-lane LDS passes alike.
+//
+// Pipeline: x and packed W run two K steps ahead (x(k+2) and W(k+3) are
+// issued at step k), scale windows one window ahead; GS = group size is a
+// template parameter so a window is a compile-time shape (K must be a
+// multiple of 256).  While the MFMAs of step k run, step k+1 is
+// dequantized into the other W stage in two halves between them: one
+// barrier per K step.
 //
 // Grid: one block per tile, M-tile fastest.  Blocks are dealt round-robin to
 // the 8 XCDs, so with 8 M-tiles (M = 2048) every XCD owns one 256-row slab of
@@ -50,7 +55,6 @@ constexpr int kThreads = 512;  // 8 waves: two per SIMD
 constexpr int kXStageBytes = BM * BK * 2;  // 32768
 constexpr int kXStages = 3;
 constexpr int kWStageBytes = BN * BK * 2;  // 16384
-constexpr size_t kLdsBytes = (size_t)kXStages * kXStageBytes + 2 * (size_t)kWStageBytes;
 
 // chunk position permutation of LDS row r (bijective on the 8 chunks; rows
 // r and r + 8 get different permutations)
@@ -113,111 +117,68 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
 
-// ---- packed W: 32 codes (one row half of a K step) = BITS words ----------
+// ---- LDS layout ----------------------------------------------------------
+//
+// [x stage 0..2: 256 rows x 128 B][dequantized W stage 0..1: 128 rows x 128 B]
+// [packed W slot 0..2: one K step, 128 rows x 8 BITS B, rows contiguous]
+// [scale window slot 0..1: 4 K steps; per 32-row quarter q: scales of its
+//  32 rows, then biases, each row kRowBytes]
 
 template <int BITS>
-struct WRegs {
-    uint32_t w[BITS];
-};
-
-// vector-memory instructions one load_words issues
+constexpr int pack_row_bytes() { return 8 * BITS; }  // 64 codes
 template <int BITS>
-constexpr int w_loads() {
-    return (BITS == 5 || BITS == 6 || BITS == 8) ? 2 : 1;
-}
-
-template <int BITS>
-__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
-                                           uint32_t* w) {
-    if constexpr (BITS == 2) {
-        v2 t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
-        w[0] = t.x; w[1] = t.y;
-    } else if constexpr (BITS == 3) {
-        v3 t = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
-        w[0] = t.x; w[1] = t.y; w[2] = t.z;
-    } else {
-        v4 t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-        w[0] = t.x; w[1] = t.y; w[2] = t.z; w[3] = t.w;
-        if constexpr (BITS == 5) {
-            w[4] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 16, soff, 0);
-        } else if constexpr (BITS == 6) {
-            v2 u = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 16, soff, 0);
-            w[4] = u.x; w[5] = u.y;
-        } else if constexpr (BITS == 8) {
-            v4 u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
-            w[4] = u.x; w[5] = u.y; w[6] = u.z; w[7] = u.w;
-        }
-    }
-}
-
-// ---- scales / biases of 4 K steps (256 codes) of one row ------------------
+constexpr int pack_slot_bytes() { return BN * pack_row_bytes<BITS>(); }
+constexpr int kPackSlots = 3;
 
 template <int GS, int SB>
-struct SWin {
-    static constexpr int kGroups = 256 / GS;                     // 8, 4, 2
-    static constexpr int kWords = kGroups * (SB == DT_F32 ? 4 : 2) / 4;
-    uint32_t s[kWords], b[kWords];
+struct Win {
+    static constexpr int kSb = SB == DT_F32 ? 4 : 2;
+    static constexpr int kGroups = 256 / GS;          // groups in 4 K steps
+    static constexpr int kRowBytes = kGroups * kSb;   // 4 .. 32
+    static constexpr int kWords = kRowBytes / 4;      // 1 .. 8
+    static constexpr int kSlotBytes = 2 * BN * kRowBytes;
 };
 
-// loads of one window: one for scales and one for biases (two each for f32
-// scales at group size 32)
-template <int GS, int SB>
-constexpr int s_loads() {
-    return SWin<GS, SB>::kWords > 4 ? 4 : 2;
+template <int BITS, int GS, int SB>
+constexpr size_t lds_bytes() {
+    return (size_t)kXStages * kXStageBytes + 2 * (size_t)kWStageBytes +
+           (size_t)kPackSlots * pack_slot_bytes<BITS>() + 2 * (size_t)Win<GS, SB>::kSlotBytes;
+}
+constexpr size_t kMaxLds = 160 * 1024;
+
+// the combinations whose buffers fit one CU's LDS (all but f32 scales at
+// group size 32 with 6- or 8-bit codes)
+template <int BITS, int GS, int SB>
+constexpr bool lds_fits() { return lds_bytes<BITS, GS, SB>() <= kMaxLds; }
+
+// ---- direct-to-LDS transfers (global_load_lds) ----------------------------
+//
+// Lane l copies E bytes to LDS address m0 + E l.  Issued through inline asm:
+// the compiler's wait-count pass would otherwise wait for these LDS writes
+// before every LDS read, prefetch included.  No other vector-memory load is
+// issued inside the K loop, so the explicit waits (wait_vmcnt) are the only
+// ones, and they count exactly.
+
+__device__ __forceinline__ void dma16(uint32_t m0v, const void* sbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0v), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
 }
 
-template <int NW>
-__device__ __forceinline__ void load_win_words(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t* w) {
-    if constexpr (NW == 1) {
-        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-    } else if constexpr (NW == 2) {
-        v2 t = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-        w[0] = t.x; w[1] = t.y;
-    } else {
-#pragma unroll
-        for (int i = 0; i < NW; i += 4) {
-            v4 t = __builtin_amdgcn_raw_buffer_load_b128(r, off + 4 * i, 0, 0);
-            w[i] = t.x; w[i + 1] = t.y; w[i + 2] = t.z; w[i + 3] = t.w;
-        }
-    }
+__device__ __forceinline__ void dma4(uint32_t m0v, const void* sbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+                 :
+                 : "s"(m0v), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
 }
 
-// scale/bias value of group i (compile-time) of a window
-template <int SB, int NW>
-__device__ __forceinline__ float win_value(const uint32_t (&w)[NW], int i) {
-    if constexpr (SB == DT_F32) return __uint_as_float(w[i]);
-    else {
-        const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
-        return SB == DT_F16 ? f16_to_f32(h) : bf16_to_f32(h);
-    }
-}
-
-// ---- per-thread staging coordinates -------------------------------------
-
-struct StageCoord {
-    uint32_t xoff[4];  // byte offset (in x) of this lane's 4 direct-to-LDS chunks, K step 0
-    uint32_t w_voff;   // byte offset of its 32 codes in W, K step 0 (dequantizing waves)
-    uint32_t sb_off;   // element index of its row's first scale
-    int w_row;         // W tile row it dequantizes
-    int w_half;        // which 32 codes of the K step
-};
-
-// x tile of K step kt straight into an LDS x stage: 4 x 16 B per lane; wave
-// w, instruction i fills the 1 KB block of rows 8 (4 w + i) .. +8 (lane l
-// writes stage + block + 16 l).  Issued through inline asm: the compiler's
-// wait-count pass would otherwise wait for these LDS writes before every LDS
-// read, prefetch included.  The caller waits for them explicitly
-// (wait_vmcnt) before the barrier that publishes the stage.
-__device__ __forceinline__ void load_x_lds(uint32_t stage_lds, const uint16_t* x, const StageCoord& c,
-                                           int wave, int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t m0v = stage_lds + (uint32_t)(4 * wave + i) * 1024u;
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                     :
-                     : "s"(m0v), "v"(c.xoff[i] + (uint32_t)kt * BK * 2), "s"(x)
-                     : "memory", "m0");
-    }
+// per-lane 64-bit address
+__device__ __forceinline__ void dma4a(uint32_t m0v, const void* addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(m0v), "v"(addr)
+                 : "memory", "m0");
 }
 
 // wait until at most N vector-memory instructions of this wave are in flight
@@ -227,43 +188,25 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// half h (0..1) of dequantizing K step j (0..3 within the scale window) into
-// W stage D: 16 codes, w_hat = fmaf(s, q, b) rounded RNE to TX
-template <int TX, int BITS, int SB, int GS, int J>
-__device__ __forceinline__ void store_half(const WRegs<BITS>& ws, const SWin<GS, SB>& sw,
-                                           uint8_t* D, const StageCoord& c, int h) {
-    float sv, bv;
-    if constexpr (GS == 32) {
-        // the thread's 32 codes are group 2J + w_half
-        const float s0 = win_value<SB>(sw.s, 2 * J), s1 = win_value<SB>(sw.s, 2 * J + 1);
-        const float b0 = win_value<SB>(sw.b, 2 * J), b1 = win_value<SB>(sw.b, 2 * J + 1);
-        sv = c.w_half ? s1 : s0;
-        bv = c.w_half ? b1 : b0;
-    } else {
-        sv = win_value<SB>(sw.s, J * 64 / GS);
-        bv = win_value<SB>(sw.b, J * 64 / GS);
-    }
-    const int sz = swz(c.w_row);
-#pragma unroll
-    for (int q = 2 * h; q < 2 * h + 2; q++) {
-        float f[8];
-        codes8<BITS>(ws.w, q, f);
-        v4 o;
-        o.x = pack2<TX>(fmaf(sv, f[0], bv), fmaf(sv, f[1], bv));
-        o.y = pack2<TX>(fmaf(sv, f[2], bv), fmaf(sv, f[3], bv));
-        o.z = pack2<TX>(fmaf(sv, f[4], bv), fmaf(sv, f[5], bv));
-        o.w = pack2<TX>(fmaf(sv, f[6], bv), fmaf(sv, f[7], bv));
-        *reinterpret_cast<v4*>(D + c.w_row * 128 + (((4 * c.w_half + q) ^ sz) << 4)) = o;
-    }
-}
+// packed W of one K step by waves 0..3: wave w copies rows 32 w .. 32 w + 31
+// (32 x 8 BITS contiguous bytes of LDS) in kInstr transfers of E bytes/lane
+template <int BITS>
+struct WDma {
+    static constexpr int E = (BITS % 4 == 0) ? 16 : 4;
+    static constexpr int kWaveBytes = 32 * pack_row_bytes<BITS>();
+    static constexpr int kInstr = kWaveBytes / (64 * E);  // 2 3 1 5 6 2 for BITS 2 3 4 5 6 8
+    static_assert(kWaveBytes % (64 * E) == 0 && pack_row_bytes<BITS>() % E == 0, "W transfer shape");
+};
+
+// ---- fragments and MFMA ----------------------------------------------------
 
 struct Frags {
     v4 a[2], b[2];
 };
 
 // fragments of k sub-step ks: A from x stage X (rows a_row + 32 i), B from W
-// stage Wt (rows b_row + 32 j); lane reads 16-byte chunk 2 ks + kh, whose
-// position is ch[ks] (all rows a lane reads share swz)
+// stage Wt (rows b_row + 32 j); lane reads 16-byte chunk 2 ks + kh at byte
+// offset chk within the row (all rows a lane reads share swz)
 __device__ __forceinline__ void read_frags(Frags& f, const uint8_t* X, const uint8_t* Wt, int a_row,
                                            int b_row, int chk) {
 #pragma unroll
@@ -280,110 +223,268 @@ __device__ __forceinline__ void mfmas(f32x16 (&acc)[2][2], const Frags& f) {
         for (int j = 0; j < 2; j++) acc[i][j] = mfma<TX>(f.a[i], f.b[j], acc[i][j]);
 }
 
-// everything a K step needs besides the accumulators and register rings
+// ---- dequantization: every thread, 16 codes of one row per K step --------
+//
+// Thread (wave w, lane l) takes row r = 16 w + l % 16 and codes
+// [16 cp, 16 cp + 16), cp = l / 16, i.e. 16-byte chunks 2 cp and 2 cp + 1 of
+// the dequantized row: 16 consecutive lanes write 16 consecutive rows.
+
+// LDS words holding the 16 codes (a 16-bit shift aligns them for odd BITS)
+template <int BITS>
+constexpr int raw_words() {
+    return BITS == 2 ? 1 : BITS == 3 ? 2 : BITS == 4 ? 2 : BITS == 5 ? 3 : BITS == 6 ? 3 : 4;
+}
+
+template <int BITS>
+__device__ __forceinline__ void read_raw(const uint8_t* pk, int r, int cp, uint32_t (&w)[raw_words<BITS>()]) {
+    // bit offset of the codes in the row: 16 cp BITS; dword aligned for even BITS
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(pk + r * pack_row_bytes<BITS>());
+    const int d0 = (16 * cp * BITS) >> 5;
+#pragma unroll
+    for (int i = 0; i < raw_words<BITS>(); i++) w[i] = row[d0 + i];
+}
+
+// 16 codes as fp32, from the raw words (shifted right by 16 for odd BITS and odd cp)
+template <int BITS>
+__device__ __forceinline__ void decode16(const uint32_t (&raw)[raw_words<BITS>()], int cp, float (&q)[16]) {
+    constexpr int NR = raw_words<BITS>();
+    uint32_t w[NR];
+    if constexpr (BITS & 1) {
+        const int sh = (cp & 1) << 4;
+#pragma unroll
+        for (int i = 0; i + 1 < NR; i++) w[i] = __builtin_amdgcn_alignbit(raw[i + 1], raw[i], sh);
+        w[NR - 1] = raw[NR - 1] >> sh;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NR; i++) w[i] = raw[i];
+    }
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                q[8 * i + 2 * j] = (float)((lo >> (8 * j)) & 0xffu);
+                q[8 * i + 2 * j + 1] = (float)((hi >> (8 * j)) & 0xffu);
+            }
+        }
+    } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) q[j] = (float)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int bit = j * BITS, wi = bit >> 5, s = bit & 31;
+            constexpr uint32_t mask = (1u << BITS) - 1u;
+            // a code straddling two words: funnel shift (v_alignbit_b32)
+            const uint32_t v = (s + BITS <= 32) ? (w[wi] >> s) & mask
+                                                : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], s) & mask;
+            q[j] = (float)v;
+        }
+    }
+}
+
+template <int SB>
+__device__ __forceinline__ float sb_load(const uint8_t* p) {
+    if constexpr (SB == DT_F32) return *reinterpret_cast<const float*>(p);
+    else if constexpr (SB == DT_F16) return f16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+    else return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+}
+
+// scale and bias of the thread's codes in window step J
+template <int GS, int SB, int J>
+__device__ __forceinline__ void read_sb(const uint8_t* win, int r, int cp, float& s, float& b) {
+    using Wn = Win<GS, SB>;
+    const int i = (J * 64 + 16 * cp) / GS;  // group within the window
+    const uint8_t* p = win + (r >> 5) * (2 * 32 * Wn::kRowBytes) + (r & 31) * Wn::kRowBytes + i * Wn::kSb;
+    s = sb_load<SB>(p);
+    b = sb_load<SB>(p + 32 * Wn::kRowBytes);
+}
+
+// half h: chunk 2 cp + h of row r = codes 8 h .. 8 h + 7 of the 16, as
+// fmaf(s, q, b) rounded RNE to TX, into W stage D
+template <int TX>
+__device__ __forceinline__ void deq_half(const float (&q)[16], float s, float b, uint8_t* D, int r, int cp,
+                                         int h) {
+    v4 o;
+    o.x = pack2<TX>(fmaf(s, q[8 * h + 0], b), fmaf(s, q[8 * h + 1], b));
+    o.y = pack2<TX>(fmaf(s, q[8 * h + 2], b), fmaf(s, q[8 * h + 3], b));
+    o.z = pack2<TX>(fmaf(s, q[8 * h + 4], b), fmaf(s, q[8 * h + 5], b));
+    o.w = pack2<TX>(fmaf(s, q[8 * h + 6], b), fmaf(s, q[8 * h + 7], b));
+    *reinterpret_cast<v4*>(D + r * 128 + (((2 * cp + h) ^ swz(r)) << 4)) = o;
+}
+
+// ---- the K loop ------------------------------------------------------------
+
+// everything a K step needs besides the accumulators
 struct Ctx {
-    uint8_t* xl;        // x stages
-    uint32_t xl_lds;    // their LDS address
-    uint8_t* wl;        // W stages
+    uint8_t* lds;
+    uint32_t lds_addr;  // LDS address of lds (low 32 bits of the flat address)
     const uint16_t* x;
-    __amdgpu_buffer_rsrc_t wr, sr, br;
-    StageCoord c;
-    int wave, KT, a_row, b_row;
+    const uint32_t* wq;
+    uint32_t xoff[4];   // byte offset (in x) of this lane's 4 x chunks, K step 0
+    int wave, lane, KT, n0, N, G;
+    uint32_t row_bytes;
+    int a_row, b_row;
     int chk[4];         // byte offset of this lane's fragment chunk, per k sub-step
+    int dr, dcp;        // dequantization: row and code quarter
 };
 
-// MFMAs of one K step (fragments of sub-step ks+1 are read while those of ks
-// are used); dequantizing waves write the next K step (ws, window step J)
-// into W stage D in two halves between them (after the last step this
-// writes a stage nobody reads)
-template <int TX, int BITS, int SB, int GS, bool DEQ, int J>
-__device__ __forceinline__ void kstep(f32x16 (&acc)[2][2], const Ctx& t, const uint8_t* X,
-                                      const uint8_t* Wt, uint8_t* D, const WRegs<BITS>& ws,
-                                      const SWin<GS, SB>& sw) {
-    Frags f0, f1;
-    read_frags(f0, X, Wt, t.a_row, t.b_row, t.chk[0]);
-    read_frags(f1, X, Wt, t.a_row, t.b_row, t.chk[1]);
-    mfmas<TX>(acc, f0);
-    read_frags(f0, X, Wt, t.a_row, t.b_row, t.chk[2]);
-    mfmas<TX>(acc, f1);
-    if constexpr (DEQ) store_half<TX, BITS, SB, GS, J>(ws, sw, D, t.c, 0);
-    read_frags(f1, X, Wt, t.a_row, t.b_row, t.chk[3]);
-    mfmas<TX>(acc, f0);
-    mfmas<TX>(acc, f1);
-    if constexpr (DEQ) store_half<TX, BITS, SB, GS, J>(ws, sw, D, t.c, 1);
+template <int BITS, int GS, int SB>
+struct Off {
+    static constexpr int kX = 0;
+    static constexpr int kW = kXStages * kXStageBytes;
+    static constexpr int kPack = kW + 2 * kWStageBytes;
+    static constexpr int kWin = kPack + kPackSlots * pack_slot_bytes<BITS>();
+};
+
+// x tile of K step kt into x stage xs: wave w, instruction i fills the 1 KB
+// block of rows 8 (4 w + i) .. +8
+__device__ __forceinline__ void load_x(const Ctx& t, int xs, int kt) {
+    const uint32_t base = t.lds_addr + (uint32_t)xs * kXStageBytes + (uint32_t)t.wave * 4096u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16(base + 1024u * i, t.x, t.xoff[i] + (uint32_t)kt * BK * 2);
 }
 
 // K step kt (P = kt % 4).  x stage kt % 3 and W stage kt % 2 hold step kt;
-// W of step kt+1 is in register slot ws[(P+1) % 4], its scales in window
-// cur.  Dequantizing waves issue the W loads of step kt+4 (slot ws[P]) and
-// at P = 0 the scale window of steps kt+4 .. kt+7 (nxt); at P = 3 the next
-// window becomes current.  Then the MFMAs with the dequantization of step
-// kt+1, the x load of step kt+2, a wait until x of step kt+1 and everything
-// issued before it has landed, and the barrier.  Loads past the last step
-// re-read the last step (never used), so every step issues the same loads.
-// In flight at the wait, after x(kt+1) [end of step kt-1]: W(kt+4) and, at
-// P = 0, the new window, then x(kt+2) [step kt].
-template <int TX, int BITS, int SB, int GS, bool DEQ, int P>
-__device__ __forceinline__ void ring_step(f32x16 (&acc)[2][2], const Ctx& t, WRegs<BITS> (&ws)[4],
-                                          SWin<GS, SB>& cur, SWin<GS, SB>& nxt, int kt) {
+// packed slot (kt+1) % 3 and window slot ((kt+1) / 4) % 2 hold the codes and
+// scales of step kt+1.  Issue x(kt+2) into x stage (kt+2) % 3; waves 0..3
+// (ROLE 0) issue the packed W of step kt+3 into slot kt % 3, waves 4..7
+// (ROLE 1) at P = 0 the scale window of steps kt+4 .. kt+7.  Then the MFMAs
+// of step kt with the dequantization of step kt+1 into W stage (kt+1) % 2,
+// the wait, the barrier.  At the wait, ROLE 0 needs x(kt+1) and W(kt+2)
+// (issued at step kt-1) landed: in flight may stay x(kt+2), W(kt+3).  ROLE 1
+// needs x(kt+1): in flight may stay x(kt+2), the window of step kt (P = 0)
+// and the one of step kt-1 (P = 1), which is first read at step kt+3 after
+// the barrier of step kt+2.  Loads past the last step re-read the last step
+// or window (never used), so every step issues the same loads.
+template <int TX, int BITS, int SB, int GS, int ROLE, int P>
+__device__ __forceinline__ void ring_step(f32x16 (&acc)[2][2], const Ctx& t, const uint32_t* wv,
+                                          const uint8_t* const* sp, int kt) {
+    using Lo = Off<BITS, GS, SB>;
+    using Wn = Win<GS, SB>;
     const int xi = kt % 3;
-    const uint8_t* X = t.xl + xi * kXStageBytes;
-    const uint8_t* Wt = t.wl + (P & 1) * kWStageBytes;
-    uint8_t* D = t.wl + ((P + 1) & 1) * kWStageBytes;
-    if constexpr (DEQ) {
-        load_words<BITS>(t.wr, t.c.w_voff, (uint32_t)min(kt + 4, t.KT - 1) * 8 * BITS, ws[P].w);
-        if constexpr (P == 0) {
-            constexpr int kG = SWin<GS, SB>::kGroups, kW = SWin<GS, SB>::kWords;
-            const uint32_t g0 = t.c.sb_off + (uint32_t)min(kt + 4, t.KT - 4) / 4 * kG;
-            load_win_words<kW>(t.sr, g0 * (SB == DT_F32 ? 4 : 2), nxt.s);
-            load_win_words<kW>(t.br, g0 * (SB == DT_F32 ? 4 : 2), nxt.b);
+    load_x(t, xi == 0 ? 2 : xi - 1, min(kt + 2, t.KT - 1));
+    if constexpr (ROLE == 0) {
+        // packed W of step kt+3 into slot kt % 3
+        using WD = WDma<BITS>;
+        const uint32_t base = t.lds_addr + Lo::kPack + (uint32_t)xi * pack_slot_bytes<BITS>() +
+                              (uint32_t)t.wave * WD::kWaveBytes;
+        const uint32_t koff = (uint32_t)min(kt + 3, t.KT - 1) * pack_row_bytes<BITS>();
+#pragma unroll
+        for (int j = 0; j < WD::kInstr; j++) {
+            if constexpr (WD::E == 16) dma16(base + 64u * 16u * j, t.wq, wv[j] + koff);
+            else dma4(base + 64u * 4u * j, t.wq, wv[j] + koff);
         }
-        if constexpr (P == 3) cur = nxt;
+    } else if constexpr (P == 0) {
+        // scale window of steps kt+4 .. kt+7 into window slot (kt/4 + 1) % 2
+        const int wi = min(kt / 4 + 1, t.KT / 4 - 1);
+        const uint32_t base = t.lds_addr + Lo::kWin + (uint32_t)(((kt >> 2) + 1) & 1) * Wn::kSlotBytes +
+                              (uint32_t)(t.wave - 4) * (2 * 32 * Wn::kRowBytes);
+        const size_t goff = (size_t)wi * Wn::kRowBytes;
+#pragma unroll
+        for (int j = 0; j < Wn::kWords; j++) dma4a(base + 256u * j, sp[j] + goff);
     }
-    kstep<TX, BITS, SB, GS, DEQ, (P + 1) & 3>(acc, t, X, Wt, D, ws[(P + 1) & 3], cur);
-    // x is issued last: the compiler does not see these loads, so the waits
-    // it adds before using W registers count only its own loads; issued
-    // earlier, x(kt+2) would sit inside those waits and be drained at once
-    load_x_lds(t.xl_lds + (uint32_t)(xi == 0 ? 2 : xi - 1) * kXStageBytes, t.x, t.c, t.wave,
-               min(kt + 2, t.KT - 1));
-    if constexpr (DEQ)
-        wait_vmcnt<4 + w_loads<BITS>() + s_loads<GS, SB>() * (P == 0)>();
-    else
-        wait_vmcnt<4>();
+    const uint8_t* X = t.lds + Lo::kX + xi * kXStageBytes;
+    const uint8_t* Wt = t.lds + Lo::kW + (P & 1) * kWStageBytes;
+    uint8_t* D = t.lds + Lo::kW + ((P + 1) & 1) * kWStageBytes;
+    const uint8_t* pk = t.lds + Lo::kPack + ((kt + 1) % 3) * pack_slot_bytes<BITS>();
+    const uint8_t* win = t.lds + Lo::kWin + (((kt + 1) >> 2) & 1) * Wn::kSlotBytes;
+
+    // MFMAs of step kt (fragments of sub-step ks+1 read while ks runs); the
+    // dequantization of step kt+1 in two halves between them
+    Frags f0, f1;
+    read_frags(f0, X, Wt, t.a_row, t.b_row, t.chk[0]);
+    uint32_t raw[raw_words<BITS>()];
+    read_raw<BITS>(pk, t.dr, t.dcp, raw);
+    float s, b;
+    read_sb<GS, SB, (P + 1) & 3>(win, t.dr, t.dcp, s, b);
+    read_frags(f1, X, Wt, t.a_row, t.b_row, t.chk[1]);
+    mfmas<TX>(acc, f0);
+    read_frags(f0, X, Wt, t.a_row, t.b_row, t.chk[2]);
+    float q[16];
+    decode16<BITS>(raw, t.dcp, q);
+    mfmas<TX>(acc, f1);
+    deq_half<TX>(q, s, b, D, t.dr, t.dcp, 0);
+    read_frags(f1, X, Wt, t.a_row, t.b_row, t.chk[3]);
+    mfmas<TX>(acc, f0);
+    deq_half<TX>(q, s, b, D, t.dr, t.dcp, 1);
+    mfmas<TX>(acc, f1);
+
+    if constexpr (ROLE == 0) wait_vmcnt<4 + WDma<BITS>::kInstr>();
+    else wait_vmcnt<4 + Wn::kWords * ((P == 0) + (P == 1))>();
     __syncthreads();
 }
 
-// prologue and main loop of one wave role
-template <int TX, int BITS, int SB, int GS, bool DEQ>
-__device__ __forceinline__ void main_loop(f32x16 (&acc)[2][2], const Ctx& t) {
-    WRegs<BITS> ws[4];
-    SWin<GS, SB> cur, nxt;
-    // prologue: x of steps 0, 1 into x stages 0, 1; W of steps 0..3 and the
-    // scale window of steps 0..3 into registers; step 0 dequantized into W
-    // stage 0
-    load_x_lds(t.xl_lds, t.x, t.c, t.wave, 0);
-    load_x_lds(t.xl_lds + kXStageBytes, t.x, t.c, t.wave, min(1, t.KT - 1));
-    if constexpr (DEQ) {
+// prologue and K loop of one wave role
+template <int TX, int BITS, int SB, int GS, int ROLE>
+__device__ __forceinline__ void main_loop(f32x16 (&acc)[2][2], const Ctx& t, const void* scales,
+                                          const void* biases) {
+    using Lo = Off<BITS, GS, SB>;
+    using Wn = Win<GS, SB>;
+    using WD = WDma<BITS>;
+    // per-lane global offsets of this role's transfers
+    uint32_t wv[ROLE == 0 ? WD::kInstr : 1];
+    const uint8_t* sp[ROLE == 1 ? Wn::kWords : 1];
+    if constexpr (ROLE == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            load_words<BITS>(t.wr, t.c.w_voff, (uint32_t)min(j, t.KT - 1) * 8 * BITS, ws[j].w);
-        constexpr int kW = SWin<GS, SB>::kWords;
-        load_win_words<kW>(t.sr, t.c.sb_off * (SB == DT_F32 ? 4 : 2), cur.s);
-        load_win_words<kW>(t.br, t.c.sb_off * (SB == DT_F32 ? 4 : 2), cur.b);
+        for (int j = 0; j < WD::kInstr; j++) {
+            const int off = 64 * WD::E * j + WD::E * t.lane;  // byte in the wave's 32 rows
+            const int row = off / pack_row_bytes<BITS>(), byte = off % pack_row_bytes<BITS>();
+            const int n = min(t.n0 + 32 * t.wave + row, t.N - 1);  // rows past N: valid data, never stored
+            wv[j] = (uint32_t)n * t.row_bytes + (uint32_t)byte;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < Wn::kWords; j++) {
+            const int d = 64 * j + t.lane;  // dword of the quarter's window part
+            const int a = d / (32 * Wn::kWords), rem = d % (32 * Wn::kWords);
+            const int row = rem / Wn::kWords, word = rem % Wn::kWords;
+            const int n = min(t.n0 + 32 * (t.wave - 4) + row, t.N - 1);
+            sp[j] = static_cast<const uint8_t*>(a ? biases : scales) + (size_t)n * t.G * Wn::kSb + 4 * word;
+        }
+    }
+
+    // prologue: x of steps 0, 1; packed W of steps 0..2 (slots 0..2); scale
+    // window 0 (slot 0); then step 0 dequantized into W stage 0
+    load_x(t, 0, 0);
+    load_x(t, 1, 1);
+    if constexpr (ROLE == 0) {
+#pragma unroll
+        for (int st = 0; st < 3; st++) {
+            const uint32_t base = t.lds_addr + Lo::kPack + (uint32_t)st * pack_slot_bytes<BITS>() +
+                                  (uint32_t)t.wave * WD::kWaveBytes;
+#pragma unroll
+            for (int j = 0; j < WD::kInstr; j++) {
+                const uint32_t v = wv[j] + (uint32_t)st * pack_row_bytes<BITS>();
+                if constexpr (WD::E == 16) dma16(base + 64u * 16u * j, t.wq, v);
+                else dma4(base + 64u * 4u * j, t.wq, v);
+            }
+        }
+    } else {
+        const uint32_t base = t.lds_addr + Lo::kWin + (uint32_t)(t.wave - 4) * (2 * 32 * Wn::kRowBytes);
+#pragma unroll
+        for (int j = 0; j < Wn::kWords; j++) dma4a(base + 256u * j, sp[j]);
     }
     wait_vmcnt<0>();
-    if constexpr (DEQ) {
-        store_half<TX, BITS, SB, GS, 0>(ws[0], cur, t.wl, t.c, 0);
-        store_half<TX, BITS, SB, GS, 0>(ws[0], cur, t.wl, t.c, 1);
+    __syncthreads();
+    {
+        uint32_t raw[raw_words<BITS>()];
+        read_raw<BITS>(t.lds + Lo::kPack, t.dr, t.dcp, raw);
+        float s, b, q[16];
+        read_sb<GS, SB, 0>(t.lds + Lo::kWin, t.dr, t.dcp, s, b);
+        decode16<BITS>(raw, t.dcp, q);
+        deq_half<TX>(q, s, b, t.lds + Lo::kW, t.dr, t.dcp, 0);
+        deq_half<TX>(q, s, b, t.lds + Lo::kW, t.dr, t.dcp, 1);
     }
     __syncthreads();
 
     // KT is a multiple of 4 (K % 256 == 0)
     for (int kt = 0; kt < t.KT; kt += 4) {
-        ring_step<TX, BITS, SB, GS, DEQ, 0>(acc, t, ws, cur, nxt, kt);
-        ring_step<TX, BITS, SB, GS, DEQ, 1>(acc, t, ws, cur, nxt, kt + 1);
-        ring_step<TX, BITS, SB, GS, DEQ, 2>(acc, t, ws, cur, nxt, kt + 2);
-        ring_step<TX, BITS, SB, GS, DEQ, 3>(acc, t, ws, cur, nxt, kt + 3);
+        ring_step<TX, BITS, SB, GS, ROLE, 0>(acc, t, wv, sp, kt);
+        ring_step<TX, BITS, SB, GS, ROLE, 1>(acc, t, wv, sp, kt + 1);
+        ring_step<TX, BITS, SB, GS, ROLE, 2>(acc, t, wv, sp, kt + 2);
+        ring_step<TX, BITS, SB, GS, ROLE, 3>(acc, t, wv, sp, kt + 3);
     }
     // no LDS transfer may still be landing when the block's LDS is released
     wait_vmcnt<0>();
@@ -394,41 +495,33 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int out_dt,
     int mtiles) {
+    static_assert(lds_fits<BITS, GS, SB>(), "LDS budget");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves, 64 x 64 each
     const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
-    const int m0 = mt * BM, n0 = nt * BN;
-    const int G = K / GS;
-    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
-    const uint32_t sbsz = SB == DT_F32 ? 4 : 2;
+    const int m0 = mt * BM;
 
     Ctx t;
+    t.lds = lds;
+    t.lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     t.x = x;
+    t.wq = wq;
     t.wave = wave;
+    t.lane = lane;
     t.KT = K / BK;
-    t.wr = make_rsrc(wq, (uint32_t)((size_t)N * row_bytes));
-    t.sr = make_rsrc(scales, (uint32_t)((size_t)N * G * sbsz));
-    t.br = make_rsrc(biases, (uint32_t)((size_t)N * G * sbsz));
-    // staging.  x tile (load_x_lds): lane writes chunk position lane%8 of
-    // row r = 8 (4 wave + i) + lane/8 and so reads global chunk
-    // (lane%8) ^ swz(r) of that row.  W tile (waves 0..3, tid < 256): row
-    // (tid % 16) + 16 (tid / 32), codes [32 ((tid / 16) % 2), +32) of the K
-    // step, so 16 consecutive lanes write 16 consecutive rows.
-    {
-        const int w_row = (tid & 15) | ((tid >> 5) << 4);
-        t.c.w_row = w_row & (BN - 1);
-        t.c.w_half = (tid >> 4) & 1;
-        const int wn_glob = min(n0 + t.c.w_row, N - 1);  // rows past N: valid data, never stored
-        t.c.w_voff = (uint32_t)wn_glob * row_bytes + t.c.w_half * 4 * BITS;
-        t.c.sb_off = (uint32_t)wn_glob * G;
+    t.n0 = nt * BN;
+    t.N = N;
+    t.G = K / GS;
+    t.row_bytes = (uint32_t)K * BITS / 8;
+    // x tile: lane writes chunk position lane%8 of row r = 8 (4 wave + i) +
+    // lane/8, so it reads global chunk (lane%8) ^ swz(r) of that row
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 8 * (4 * wave + i) + (lane >> 3);
-            const int rg = min(m0 + r, M - 1);  // rows past M: valid data, never stored
-            t.c.xoff[i] = ((uint32_t)rg * K + (((lane & 7) ^ swz(r)) << 3)) * 2;
-        }
+    for (int i = 0; i < 4; i++) {
+        const int r = 8 * (4 * wave + i) + (lane >> 3);
+        const int rg = min(m0 + r, M - 1);  // rows past M: valid data, never stored
+        t.xoff[i] = ((uint32_t)rg * K + (((lane & 7) ^ swz(r)) << 3)) * 2;
     }
     // fragment addressing: lane reads row (lane % 32), k block 8 (lane / 32)
     const int fr_row = lane & 31, kh = lane >> 5;
@@ -436,10 +529,8 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     t.b_row = wn * 64 + fr_row;
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) t.chk[ks] = ((2 * ks + kh) ^ swz(fr_row)) << 4;
-    t.xl = lds;
-    t.wl = lds + kXStages * kXStageBytes;
-    // LDS address of the x stages (low 32 bits of the flat address)
-    t.xl_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)t.xl);
+    t.dr = 16 * wave + (lane & 15);
+    t.dcp = lane >> 4;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -450,13 +541,13 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
 
     if (wave < 4)
-        main_loop<TX, BITS, SB, GS, true>(acc, t);
+        main_loop<TX, BITS, SB, GS, 0>(acc, t, scales, biases);
     else
-        main_loop<TX, BITS, SB, GS, false>(acc, t);
+        main_loop<TX, BITS, SB, GS, 1>(acc, t, scales, biases);
 
     // ---- epilogue: 32x32 accumulator layout: lane holds column (lane % 32),
     // VGPR v holds row 8 (v / 4) + 4 (lane / 32) + v % 4 ----
-    const int ncol = n0 + wn * 64 + (lane & 31);
+    const int ncol = t.n0 + wn * 64 + (lane & 31);
     const int mrow = m0 + wm * 64 + 4 * (lane >> 5);
     if (out_dt == DT_BF16 || out_dt == DT_F16) {
         uint16_t* yo = static_cast<uint16_t*>(y);
@@ -491,15 +582,20 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
 
 template <int TX, int BITS, int SB, int GS>
 LuxStatus launch4(const QmmArgs& a, hipStream_t st) {
-    auto kern = qgemm_kernel<TX, BITS, SB, GS>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
-    if (attr != hipSuccess) return LuxStatus::Internal;
-    const int mtiles = (a.M + BM - 1) / BM, ntiles = (a.N + BN - 1) / BN;
-    hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(kThreads), kLdsBytes, st,
-                       static_cast<const uint16_t*>(a.x), a.wq, a.scales, a.biases, a.y, a.M, a.K,
-                       a.N, a.out_dtype, mtiles);
-    return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+    if constexpr (!lds_fits<BITS, GS, SB>()) {
+        return LuxStatus::NotSupported;
+    } else {
+        auto kern = qgemm_kernel<TX, BITS, SB, GS>;
+        constexpr size_t lds = lds_bytes<BITS, GS, SB>();
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return LuxStatus::Internal;
+        const int mtiles = (a.M + BM - 1) / BM, ntiles = (a.N + BN - 1) / BN;
+        hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(kThreads), lds, st,
+                           static_cast<const uint16_t*>(a.x), a.wq, a.scales, a.biases, a.y, a.M, a.K,
+                           a.N, a.out_dtype, mtiles);
+        return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+    }
 }
 
 template <int TX, int BITS, int GS>

@@ -139,8 +139,10 @@ class Context:
         _check(self.q.op_quantize(self.handle, w.handle, w_q.handle, scales.handle, biases.handle,
                                   N, K, group_size, bits, w_dtype, sb_dtype), "op_quantize")
 
-    def select_kernel(self, M, K, N, group_size, bits, x_dtype) -> int:
-        return self.q.select_kernel(M, K, N, group_size, bits, x_dtype)
+    def select_kernel(self, M, K, N, group_size, bits, x_dtype, sb_dtype=None) -> int:
+        """The kernel AUTO runs for this shape; sb_dtype defaults to x_dtype."""
+        return self.q.select_kernel(M, K, N, group_size, bits, x_dtype,
+                                    x_dtype if sb_dtype is None else sb_dtype)
 
 
 def esize(dtype: int) -> int:

@@ -94,9 +94,14 @@ def test_quant_extension_table_without_gpu():
     assert q.ext_version == abi.QUANT_EXT_VERSION
     assert q.struct_size == ctypes.sizeof(abi.QuantVtbl)
     # kernel selection is pure host logic
-    assert q.select_kernel(1, 4096, 14336, 64, 4, abi.FLOAT16) == abi.KERNEL_GEMV
-    assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.BFLOAT16) == abi.KERNEL_GEMM
-    assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.FLOAT32) == abi.KERNEL_GEMV
+    assert q.select_kernel(1, 4096, 14336, 64, 4, abi.FLOAT16, abi.FLOAT16) == abi.KERNEL_GEMV
+    assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.BFLOAT16, abi.BFLOAT16) == abi.KERNEL_GEMM
+    assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.FLOAT32, abi.FLOAT32) == abi.KERNEL_GEMV
+    # K not a multiple of 256, and f32 scales at group 32 with 8-bit codes,
+    # stay on the GEMV
+    assert q.select_kernel(2048, 4160, 4096, 64, 4, abi.BFLOAT16, abi.BFLOAT16) == abi.KERNEL_GEMV
+    assert q.select_kernel(2048, 4096, 4096, 32, 8, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMV
+    assert q.select_kernel(2048, 4096, 4096, 32, 4, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMM
     # NULL context / buffers are rejected before any device work
     assert q.op_quantized_matmul(None, None, None, None, None, None, 1, 64, 1, 64, 4, 1, 1, 1) == \
         abi.ERR_INVALID_ARGUMENT

@@ -222,10 +222,18 @@ def test_gemm_parity(ctx, oracle, bits, xd, sbd, od):
     """The GEMM equals the oracle's "dequantize to T, then matmul" form
     (w_round = x dtype) to the dtype gates; ragged M and N exercise the
     tile edges."""
+    from mlx_amd import abi, runtime
     O = oracle
     for (M, K, N, gs) in [(300, 512, 200, 64), (256, 1024, 128, 32), (33, 256, 130, 128),
                           (512, 768, 384, 64)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 17 + M)
+        if sbd == F32 and gs == 32 and bits >= 6:
+            # the GEMM's LDS buffers do not fit one CU for this combination
+            with pytest.raises(runtime.LuxError) as e:
+                run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+            assert e.value.code == abi.ERR_NOT_SUPPORTED
+            assert ctx.select_kernel(M, K, N, gs, bits, xd, sbd) == abi.KERNEL_GEMV
+            continue
         y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, w_round=xd)
         check_output(O, y, want, od, f"gemm b{bits} M{M} K{K} N{N} g{gs}")
