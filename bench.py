@@ -276,7 +276,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(GEMV_PROFILE),
-                     "kernel": "qgemv_reg_kernel", "kernel_us_avg": round(r["kernel_ms_avg"] * 1e3, 3),
+                     "kernel": "qgemv_stream_kernel", "kernel_us_avg": round(r["kernel_ms_avg"] * 1e3, 3),
                      "kernel_us_single_launch": round(r["single_ms_avg"] * 1e3, 3),
                      "algorithmic_bytes": wb},
     }

@@ -3,7 +3,8 @@
 // Implements the Lux GPU backend plugin ABI v2 (include/lux_gpu_backend_abi.h,
 // layout-identical to reference include/lux/gpu/backend_plugin.h) over HIP:
 //   context = one gfx950 device + one non-blocking stream,
-//   buffer  = one hipMalloc allocation,
+//   buffer  = one hipMalloc allocation with kTailPad zeroed bytes of slack
+//             past its end (kernels may read whole 16-byte chunks there),
 // and the additive quantized-matmul extension (include/lux_gpu_quant_backend.h).
 //
 // Semantics follow the reference's built-in CPU backend where the ABI leaves
@@ -150,13 +151,13 @@ LuxBackendBuffer* hip_buffer_alloc(LuxBackendContext* c, size_t bytes) {
     if (!b) return nullptr;
     b->size = bytes;
     if (bytes) {
-        if (hipMalloc(&b->ptr, bytes) != hipSuccess) {
+        if (hipMalloc(&b->ptr, bytes + lxq::kTailPad) != hipSuccess) {
             delete b;
             return nullptr;
         }
-        // zero-filled like the reference CPU backend (src/cpu_backend.cpp:129);
-        // ordered before any later work on the context stream
-        if (hipMemsetAsync(b->ptr, 0, bytes, ctx->stream) != hipSuccess) {
+        // zero-filled like the reference CPU backend (src/cpu_backend.cpp:129),
+        // tail slack included; ordered before any later work on the context stream
+        if (hipMemsetAsync(b->ptr, 0, bytes + lxq::kTailPad, ctx->stream) != hipSuccess) {
             hipFree(b->ptr);
             delete b;
             return nullptr;
@@ -173,12 +174,13 @@ LuxBackendBuffer* hip_buffer_alloc_with_data(LuxBackendContext* c, const void* d
     if (!b) return nullptr;
     b->size = bytes;
     if (bytes) {
-        if (hipMalloc(&b->ptr, bytes) != hipSuccess) {
+        if (hipMalloc(&b->ptr, bytes + lxq::kTailPad) != hipSuccess) {
             delete b;
             return nullptr;
         }
         // the caller may free `data` on return: copy synchronously
-        if (hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        if (hipMemsetAsync(static_cast<uint8_t*>(b->ptr) + bytes, 0, lxq::kTailPad, ctx->stream) != hipSuccess ||
+            hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
             hipStreamSynchronize(ctx->stream) != hipSuccess) {
             hipFree(b->ptr);
             delete b;

@@ -10,6 +10,12 @@ namespace lxq {
 
 enum class LuxStatus : int { Ok = 0, Invalid = 1, OutOfMemory = 2, NotSupported = 3, Internal = 5 };
 
+// Every device buffer handed to these launchers is followed by at least
+// kTailPad readable bytes (the plugin allocates them, zero-filled), so a
+// kernel may copy an array whose size is not a multiple of 16 bytes in whole
+// 16-byte chunks.
+constexpr size_t kTailPad = 256;
+
 struct QmmArgs {
     const void* x;        // [M, K] x_dtype
     const uint32_t* wq;   // [N, K*bits/32]

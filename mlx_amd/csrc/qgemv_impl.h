@@ -200,215 +200,425 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Register-x variant for K <= 4096 (one 64-code unit per lane) and M <= 4:
-// each wave owns R consecutive rows.  It issues its x loads first (L2
-// hits), then the weight loads of all R rows, then computes row r as soon
-// as row r has arrived, so the other rows' HBM traffic overlaps the math.
-// No LDS and no barriers.
+// Streaming kernel for K <= 4096 (one 64-code unit per lane): M <= 4 with
+// 16-bit x, M == 1 with f32 x.
+//
+// A block is 4 waves (one per SIMD); wave w owns R consecutive rows.  Per
+// block, x and the scale/bias rows of the block's 4R rows are copied into
+// LDS by buffer->LDS DMA, once.  Each wave then loads its rows' packed
+// words straight into registers (buffer loads: wave-uniform row offsets in
+// SGPRs, no per-lane address arithmetic) and computes row r as soon as row
+// r's loads have landed, so the HBM stream overlaps the arithmetic.  Lane
+// partials of all rows are reduced together with permlane swaps and DPP.
+//
+// Operands (exact products, fp32 accumulation):
+//   f16 x, 4-bit: a code kept in place inside a 16-bit half is an f16
+//     subnormal, value q * 2^(p-24) for bit position p: the codes at p = 0
+//     and p = 4 of each half need only a mask (the other two after one
+//     shift by 8), and sum x*v = 2^-24 (sum_{p=0} x q + 16 sum_{p=4} x q).
+//   f16 x, 8-bit: bytes 0 and 2 (and, after a shift by 8, bytes 1 and 3)
+//     are subnormals q * 2^-24.
+//   otherwise the "1 + q/2^P" operands of unit_pairs_magic (bf16 cannot use
+//     subnormals: x * q * 2^-133 underflows fp32), or fp32 FMAs for f32 x.
 // ---------------------------------------------------------------------------
 
-// x for one lane's unit: 64 values, permuted into the operand-pair order of
-// the codes, plus the sums over the two 32-value halves
-template <int BITS, int TX, bool APART>
-__device__ __forceinline__ void lane_x_pairs(const void* __restrict__ x, size_t off, uint32_t* xp,
-                                             float& h0, float& h1) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(x) + off);
-    uint32_t nat[32];
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+// a per-lane buffer offset that reads zeros: every buffer here is < 2^31 bytes
+constexpr uint32_t kZeroOff = 0x80000000u;
+
+constexpr int kStreamWaves = 4;
+
+enum : int { OP_SUB4 = 0, OP_SUB8 = 1, OP_MAGIC = 2, OP_BF16U8 = 3, OP_F32 = 4 };
+template <int BITS, int TX>
+constexpr int op_kind() {
+    return TX == DT_F32 ? OP_F32
+         : (TX == DT_F16 && BITS == 4) ? OP_SUB4
+         : (TX == DT_F16 && BITS == 8) ? OP_SUB8
+         : (TX == DT_BF16 && BITS == 8) ? OP_BF16U8
+         : OP_MAGIC;
+}
+
+// load instructions per 64-code unit (2*BITS words: 128-bit loads + one 64-bit)
+template <int BITS>
+constexpr int unit_loads() { return (2 * BITS) / 4 + ((2 * BITS) % 4 ? 1 : 0); }
+
+template <int BITS>
+__device__ __forceinline__ void load_unit_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                              uint32_t* w) {
+    constexpr int W = 2 * BITS;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        u32x4 v = p[i];
-        nat[4 * i] = v.x; nat[4 * i + 1] = v.y; nat[4 * i + 2] = v.z; nat[4 * i + 3] = v.w;
+    for (int i = 0; i + 4 <= W; i += 4) {
+        const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 4 * i, soff, 0);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
     }
-    // half sums: dot2 against (1, 1) is exact per product, fp32 accumulate
-    const uint32_t one2 = TX == DT_F16 ? 0x3C003C00u : 0x3F803F80u;
-    float a = 0.f, b = 0.f;
+    if constexpr (W % 4 == 2) {
+        const v2u32 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4 * (W - 2), soff, 0);
+        w[W - 2] = v.x; w[W - 1] = v.y;
+    }
+}
+
+template <int TX, int SB, int MR, int R>
+struct StreamLds {
+    static constexpr int kSb = SB == DT_F32 ? 4 : 2;
+    static constexpr int kXRow = (TX == DT_F32 ? 4 : 2) * 4096;  // one x row, K <= 4096
+    static constexpr int kRows = kStreamWaves * R;
+    // the block's scale rows (at most 128 groups) plus 16 B of alignment slack
+    static constexpr int kSbBytes = kRows * 128 * kSb + 16;
+    static constexpr int X = 0;
+    static constexpr int S = MR * kXRow;
+    static constexpr int B = S + kSbBytes;
+    static constexpr int BYTES = B + kSbBytes;
+};
+
+// x operands of one lane's unit for one row of x
+template <int BITS, int TX, int OP>
+struct XOps {
+    static constexpr int kRegs = OP == OP_F32 ? 64 : 32;
+    uint32_t v[kRegs];
+    float h0, h1;  // sums of x over the unit's two 32-code halves (scaled for OP_SUB*)
+    float hs;      // h0 + h1
+};
+
+template <int BITS, int TX, int OP>
+__device__ __forceinline__ void prep_x(const uint8_t* lx, XOps<BITS, TX, OP>& o) {
+    if constexpr (OP == OP_F32) {
+        const v4u32* p = reinterpret_cast<const v4u32*>(lx);
 #pragma unroll
-    for (int i = 0; i < 16; i++) a = dot2(nat[i], one2, a, TX);
-#pragma unroll
-    for (int i = 16; i < 32; i++) b = dot2(nat[i], one2, b, TX);
-    h0 = a;
-    h1 = b;
-    if constexpr (APART) {
-        // block of P codes = P/2 dwords; pair j = (x_j, x_{j+P/2})
-        constexpr int P = PairLayout<BITS>::kCodesPerWord, D = P / 2;  // dwords per block
-#pragma unroll
-        for (int blk = 0; blk < 64 / P; blk++) {
-#pragma unroll
-            for (int j = 0; j < D; j++) {
-                // element j lives in dword j/2 (half j%2); element j+P/2 in dword (j+D)/2 ... of the block
-                const int e0 = j, e1 = j + D;  // element indices within the block (D = P/2)
-                const uint32_t w0 = nat[blk * D + e0 / 2], w1 = nat[blk * D + e1 / 2];
-                const uint32_t lo = (e0 & 1) ? (w0 >> 16) : (w0 & 0xffffu);
-                const uint32_t hi = (e1 & 1) ? (w1 & 0xffff0000u) : (w1 << 16);
-                xp[blk * D + j] = lo | hi;
-            }
+        for (int i = 0; i < 16; i++) {
+            const v4u32 t = p[i];
+            o.v[4 * i] = t.x; o.v[4 * i + 1] = t.y; o.v[4 * i + 2] = t.z; o.v[4 * i + 3] = t.w;
         }
-    } else {
+        float a = 0.f, b = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) xp[i] = nat[i];
+        for (int i = 0; i < 32; i++) a += __uint_as_float(o.v[i]);
+#pragma unroll
+        for (int i = 32; i < 64; i++) b += __uint_as_float(o.v[i]);
+        o.h0 = a;
+        o.h1 = b;
+        o.hs = a + b;
+    } else {
+        uint32_t nat[32];
+        const v4u32* p = reinterpret_cast<const v4u32*>(lx);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const v4u32 t = p[i];
+            nat[4 * i] = t.x; nat[4 * i + 1] = t.y; nat[4 * i + 2] = t.z; nat[4 * i + 3] = t.w;
+        }
+        // half sums: dot2 against (1, 1) is exact per product, fp32 accumulate
+        const uint32_t one2 = TX == DT_F16 ? 0x3C003C00u : 0x3F803F80u;
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) a = dot2(nat[i], one2, a, TX);
+#pragma unroll
+        for (int i = 16; i < 32; i++) b = dot2(nat[i], one2, b, TX);
+        if constexpr (OP == OP_SUB4) {
+            // word j covers x[8j..8j+7] = nat[4j..4j+3]; operand order per word:
+            // (x0,x4) (x1,x5) (x2,x6) (x3,x7)  [mask 0xF, mask 0xF0, >>8 then the same]
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                o.v[4 * j]     = __builtin_amdgcn_perm(nat[4 * j + 2], nat[4 * j], 0x05040100u);
+                o.v[4 * j + 1] = __builtin_amdgcn_perm(nat[4 * j + 2], nat[4 * j], 0x07060302u);
+                o.v[4 * j + 2] = __builtin_amdgcn_perm(nat[4 * j + 3], nat[4 * j + 1], 0x05040100u);
+                o.v[4 * j + 3] = __builtin_amdgcn_perm(nat[4 * j + 3], nat[4 * j + 1], 0x07060302u);
+            }
+            o.h0 = a * 0x1p-24f;
+            o.h1 = b * 0x1p-24f;
+            o.hs = (a + b) * 0x1p-24f;
+        } else if constexpr (OP == OP_SUB8) {
+            // word j covers x[4j..4j+3] = nat[2j], nat[2j+1]: (x0,x2) (x1,x3)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                o.v[2 * j]     = __builtin_amdgcn_perm(nat[2 * j + 1], nat[2 * j], 0x05040100u);
+                o.v[2 * j + 1] = __builtin_amdgcn_perm(nat[2 * j + 1], nat[2 * j], 0x07060302u);
+            }
+            o.h0 = a * 0x1p-24f;
+            o.h1 = b * 0x1p-24f;
+            o.hs = (a + b) * 0x1p-24f;
+        } else {
+            constexpr bool kApart = (OP == OP_MAGIC) && PairLayout<BITS>::kApart;
+            if constexpr (kApart) {
+                // block of P codes = P/2 dwords; pair j = (x_j, x_{j+P/2})
+                constexpr int P = PairLayout<BITS>::kCodesPerWord, D = P / 2;
+#pragma unroll
+                for (int blk = 0; blk < 64 / P; blk++) {
+#pragma unroll
+                    for (int j = 0; j < D; j++) {
+                        const int e0 = j, e1 = j + D;
+                        const uint32_t w0 = nat[blk * D + e0 / 2], w1 = nat[blk * D + e1 / 2];
+                        const uint32_t lo = (e0 & 1) ? (w0 >> 16) : (w0 & 0xffffu);
+                        const uint32_t hi = (e1 & 1) ? (w1 & 0xffff0000u) : (w1 << 16);
+                        o.v[blk * D + j] = lo | hi;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; i++) o.v[i] = nat[i];
+            }
+            o.h0 = a;
+            o.h1 = b;
+            o.hs = a + b;
+        }
     }
 }
 
-// raw element i of a T_sb array (compile-time dtype: no branches, so the
-// compiler keeps every load of the wave in flight)
-template <int DT>
-__device__ __forceinline__ float load_c(const void* __restrict__ p, size_t i) {
-    if constexpr (DT == DT_F32) return reinterpret_cast<const float*>(p)[i];
-    else if constexpr (DT == DT_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-    else return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+// factor that turns the reduced lane partials into y
+template <int OP>
+constexpr float out_scale() { return (OP == OP_SUB4 || OP == OP_SUB8) ? 0x1p24f : 1.f; }
+
+// partial of one row for one row of x.  TWO (group size 32): s0/b0 cover
+// codes 0..31 and s1/b1 codes 32..63; otherwise one group covers the unit
+// and s1/b1 are unused.
+template <int BITS, int TX, int OP, bool TWO>
+__device__ __forceinline__ float row_partial(const uint32_t* w, const XOps<BITS, TX, OP>& xo, float s0,
+                                             float b0, float s1, float b1) {
+    if constexpr (OP == OP_SUB4) {
+        // a: codes at bit 0 (q * 2^-24); c: codes at bit 4 (16 q * 2^-24)
+        float a0 = 0.f, c0 = 0.f, a1 = 0.f, c1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t wj = w[j], w8 = wj >> 8;
+            float& a = (TWO && j >= 4) ? a1 : a0;
+            float& c = (TWO && j >= 4) ? c1 : c0;
+            a = dot2(xo.v[4 * j], wj & 0x000F000Fu, a, DT_F16);
+            c = dot2(xo.v[4 * j + 1], wj & 0x00F000F0u, c, DT_F16);
+            a = dot2(xo.v[4 * j + 2], w8 & 0x000F000Fu, a, DT_F16);
+            c = dot2(xo.v[4 * j + 3], w8 & 0x00F000F0u, c, DT_F16);
+        }
+        if constexpr (TWO)
+            return fmaf(s0, fmaf(c0, 0.0625f, a0), fmaf(s1, fmaf(c1, 0.0625f, a1), fmaf(b0, xo.h0, b1 * xo.h1)));
+        else
+            return fmaf(s0, fmaf(c0, 0.0625f, a0), b0 * xo.hs);
+    } else if constexpr (OP == OP_SUB8) {
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t wj = w[j], w8 = wj >> 8;
+            float& d = j < 8 ? d0 : d1;
+            d = dot2(xo.v[2 * j], wj & 0x00FF00FFu, d, DT_F16);
+            d = dot2(xo.v[2 * j + 1], w8 & 0x00FF00FFu, d, DT_F16);
+        }
+        if constexpr (TWO) return fmaf(s0, d0, fmaf(s1, d1, fmaf(b0, xo.h0, b1 * xo.h1)));
+        else return fmaf(s0, d0 + d1, b0 * xo.hs);
+    } else if constexpr (OP == OP_F32) {
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) d0 = fmaf(__uint_as_float(xo.v[i]), (float)unit_code<BITS>(w, i), d0);
+#pragma unroll
+        for (int i = 32; i < 64; i++) d1 = fmaf(__uint_as_float(xo.v[i]), (float)unit_code<BITS>(w, i), d1);
+        if constexpr (TWO) return (s0 * d0 + b0 * xo.h0) + (s1 * d1 + b1 * xo.h1);
+        else return s0 * (d0 + d1) + b0 * xo.hs;
+    } else {
+        uint32_t pr[32];
+        if constexpr (OP == OP_MAGIC)
+            unit_pairs_magic<BITS, (TX == DT_F16 ? 10 : 7)>(w, pr);
+        else
+            unit_pairs_bf16_u8(w, pr);
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) d0 = dot2(xo.v[i], pr[i], d0, TX);
+#pragma unroll
+        for (int i = 16; i < 32; i++) d1 = dot2(xo.v[i], pr[i], d1, TX);
+        if constexpr (OP == OP_MAGIC) {
+            // D = sum x v(q) = h + sum x q / kPow  =>  s sum x q + b h = (s kPow) D + (b - s kPow) h
+            constexpr float kPow = MagicCfg<BITS, (TX == DT_F16 ? 10 : 7)>::kPow;
+            if constexpr (TWO)
+                return ((s0 * kPow) * d0 + fmaf(-s0, kPow, b0) * xo.h0) +
+                       ((s1 * kPow) * d1 + fmaf(-s1, kPow, b1) * xo.h1);
+            else
+                return (s0 * kPow) * (d0 + d1) + fmaf(-s0, kPow, b0) * xo.hs;
+        } else {
+            if constexpr (TWO) return (s0 * d0 + b0 * xo.h0) + (s1 * d1 + b1 * xo.h1);
+            else return s0 * (d0 + d1) + b0 * xo.hs;
+        }
+    }
 }
 
-template <int BITS, int TX, int SB, int MR, int R>
-__global__ __launch_bounds__(kThreads) void qgemv_reg_kernel(
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Eight 64-lane sums at once.  permlane32 swaps fold value pairs into lane
+// halves, permlane16 swaps into 16-lane rows, then an 8-lane rotate merges
+// two values per row and DPP finishes each 8-lane group.  Afterwards lanes
+// with (lane & 7) == 0 hold the sum of v[sum8_index(lane)].
+__device__ __forceinline__ float sum8(const float* v, int lane) {
+    const float w0 = swap32_sum(v[0], v[1]), w1 = swap32_sum(v[2], v[3]);
+    const float w2 = swap32_sum(v[4], v[5]), w3 = swap32_sum(v[6], v[7]);
+    const float u0 = swap16_sum(w0, w1), u1 = swap16_sum(w2, w3);  // rows: v0 v2 v1 v3 / v4 v6 v5 v7
+    const bool hi = lane & 8;
+    const float a = hi ? u1 : u0, b = hi ? u0 : u1;
+    float z = a + dpp_f<0x128>(b);  // row_ror:8
+    z += dpp_f<0xB1>(z);            // quad_perm [1,0,3,2]
+    z += dpp_f<0x4E>(z);            // quad_perm [2,3,0,1]
+    z += dpp_f<0x141>(z);           // row_half_mirror
+    return z;
+}
+__device__ __host__ __forceinline__ int sum8_index(int lane) {
+    const int row = lane >> 4, half = (lane >> 3) & 1;
+    return 4 * half + (((row & 1) << 1) | (row >> 1));
+}
+
+template <int BITS, int TX, int SB, int MR, int R, bool TWO>
+__global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int gsize,
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int gshift,
     int out_dt) {
-    constexpr bool kMagic = (TX != DT_F32) && !(TX == DT_BF16 && BITS == 8);
-    constexpr bool kApartX = kMagic && PairLayout<BITS>::kApart;
-    constexpr float kPow = MagicCfg<BITS, (TX == DT_F16 ? 10 : 7)>::kPow;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n0 = (blockIdx.x * (kThreads / 64) + wave) * R;
-    if (n0 >= N) return;  // wave-uniform
+    using L = StreamLds<TX, SB, MR, R>;
+    constexpr int OP = op_kind<BITS, TX>();
+    constexpr int XE = TX == DT_F32 ? 4 : 2;
+    constexpr int W = 2 * BITS;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[L::BYTES];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int units = K >> 6;
     const bool active = lane < units;
-    // loads are unconditional: idle lanes and rows past N read clamped (valid)
-    // addresses and their results are never stored
     const int u = active ? lane : units - 1;
-    const int G = K / gsize;
-    const int row_words = (K * BITS) >> 5;
-    const int g0 = (u * 64) / gsize;
-    const int g1 = g0 + (gsize == 32 ? 1 : 0);
+    const int G = K >> gshift;  // groups per row; group size 1 << gshift
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+    const uint32_t sb_row = (uint32_t)G * L::kSb;
+    const int nb0 = blockIdx.x * L::kRows;
+    const int n0 = nb0 + wave * R;
 
-    // ---- x first (L2-resident, shared by every wave) ----
-    uint32_t xp[MR][32];
-    float xf[TX == DT_F32 ? MR : 1][TX == DT_F32 ? 64 : 1];
-    float h0[MR], h1[MR];
+    // ---- 1. x rows (zeros past K and past M) and the block's scale/bias rows into LDS ----
+    const uint32_t sb_first = (uint32_t)nb0 * sb_row, sb_base = sb_first & ~15u;
+    {
+        const auto xr = buf_rsrc(x, (uint32_t)M * K * XE);
+        constexpr int XC = MR * L::kXRow / 16;  // 16-byte chunks
+        const int kc = K * XE / 16;            // chunks of one x row
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-        const int mc = m < M ? m : M - 1;
-        if constexpr (TX == DT_F32) {
-            const u32x4* p = reinterpret_cast<const u32x4*>(
-                reinterpret_cast<const float*>(x) + (size_t)mc * K + u * 64);
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                u32x4 v = p[i];
-                xf[m][4 * i] = __uint_as_float(v.x); xf[m][4 * i + 1] = __uint_as_float(v.y);
-                xf[m][4 * i + 2] = __uint_as_float(v.z); xf[m][4 * i + 3] = __uint_as_float(v.w);
+        for (int c0 = 0; c0 < XC; c0 += 64 * kStreamWaves) {
+            const int cw = c0 + wave * 64, c = cw + lane;
+            const int m = c / (L::kXRow / 16), cc = c % (L::kXRow / 16);
+            const uint32_t voff = (cc < kc && m < M) ? (uint32_t)(m * K * XE + cc * 16) : kZeroOff;
+            if (cw < XC)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(lds + L::X + cw * 16), 16, voff, 0, 0, 0);
+        }
+        // whole 16-byte chunks: the last one may run into the buffer's tail slack
+        const uint32_t sbytes = ((uint32_t)N * sb_row + 15u) & ~15u;
+        const auto sr = buf_rsrc(scales, sbytes), br = buf_rsrc(biases, sbytes);
+        const int sc = (int)((sb_first - sb_base + L::kRows * sb_row + 15) / 16);
+        for (int cw = wave * 64; cw < sc; cw += 64 * kStreamWaves) {
+            if (cw + lane < sc) {
+                const uint32_t voff = sb_base + (uint32_t)(cw + lane) * 16;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_ptr)(lds + L::S + cw * 16), 16, voff, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_ptr)(lds + L::B + cw * 16), 16, voff, 0, 0, 0);
             }
-        } else {
-            lane_x_pairs<BITS, TX, kApartX>(x, (size_t)mc * K + u * 64, xp[m], h0[m], h1[m]);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- weight loads of all R rows ----
-    uint32_t wv[R][2 * BITS];
-    float sc[R][2], bi[R][2];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int n = (n0 + r < N) ? n0 + r : N - 1;
-        load_unit<BITS>(wq + (size_t)n * row_words + (size_t)u * 2 * BITS, wv[r]);
-        sc[r][0] = load_c<SB>(scales, (size_t)n * G + g0);
-        bi[r][0] = load_c<SB>(biases, (size_t)n * G + g0);
-    }
-    // group 32: the unit's second half has its own scale and bias
-    if (gsize == 32) {
+    // ---- 2. this wave's rows into registers; rows past N re-read row N-1
+    // (never stored), idle lanes read zeros ----
+    uint32_t w[R][W];
+    {
+        const auto wr = buf_rsrc(wq, (uint32_t)N * row_bytes);
+        const uint32_t voff = active ? (uint32_t)lane * (8 * BITS) : kZeroOff;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int n = (n0 + r < N) ? n0 + r : N - 1;
-            sc[r][1] = load_c<SB>(scales, (size_t)n * G + g1);
-            bi[r][1] = load_c<SB>(biases, (size_t)n * G + g1);
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            sc[r][1] = sc[r][0];
-            bi[r][1] = bi[r][0];
+            const int n = n0 + r < N ? n0 + r : N - 1;
+            load_unit_buf<BITS>(wr, voff, (uint32_t)n * row_bytes, w[r]);
         }
     }
-
-    if constexpr (TX == DT_F32) {
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            float a = 0.f, b = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; i++) a += xf[m][i];
-#pragma unroll
-            for (int i = 32; i < 64; i++) b += xf[m][i];
-            h0[m] = a;
-            h1[m] = b;
-        }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- 3. this wave's DMA was issued before its NW weight loads: wait for
+    // it, then the barrier publishes every wave's part ----
+    {
+        constexpr int NW = R * unit_loads<BITS>();
+        static_assert(NW < 64, "vmcnt holds 6 bits");
+        __builtin_amdgcn_s_waitcnt((NW & 0xF) | ((NW >> 4) << 14) | (0x7 << 4) | (0xF << 8));
     }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
 
-    float acc[R][MR];
+    // ---- 4. x operands ----
+    XOps<BITS, TX, OP> xo[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) prep_x<BITS, TX, OP>(lds + L::X + m * L::kXRow + u * 64 * XE, xo[m]);
+
+    // ---- 5. rows in arrival order ----
+    // the unit's first group (codes 64u..): group size 32 -> 2u (and 2u+1)
+    const int g0 = (u << 6) >> gshift;
+    const uint8_t* ls = lds + L::S + (sb_first - sb_base) + (size_t)(wave * R) * sb_row + g0 * L::kSb;
+    const uint8_t* lb = lds + L::B + (sb_first - sb_base) + (size_t)(wave * R) * sb_row + g0 * L::kSb;
+    constexpr int V = R * MR, VP = (V + 7) / 8 * 8;
+    float acc[VP];
+#pragma unroll
+    for (int i = 0; i < VP; i++) acc[i] = 0.f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        if constexpr (TX == DT_F32) {
-            float q[64];
-#pragma unroll
-            for (int i = 0; i < 64; i++) q[i] = (float)unit_code<BITS>(wv[r], i);
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-                for (int i = 0; i < 32; i++) d0 = fmaf(xf[m][i], q[i], d0);
-#pragma unroll
-                for (int i = 32; i < 64; i++) d1 = fmaf(xf[m][i], q[i], d1);
-                acc[r][m] = (sc[r][0] * d0 + bi[r][0] * h0[m]) + (sc[r][1] * d1 + bi[r][1] * h1[m]);
-            }
+        float s0, b0, s1 = 0.f, b1 = 0.f;
+        if constexpr (SB == DT_F32) {
+            const float* ps = reinterpret_cast<const float*>(ls + r * sb_row);
+            const float* pb = reinterpret_cast<const float*>(lb + r * sb_row);
+            s0 = ps[0];
+            b0 = pb[0];
+            if constexpr (TWO) { s1 = ps[1]; b1 = pb[1]; }
         } else {
-            uint32_t pr[32];
-            if constexpr (kMagic)
-                unit_pairs_magic<BITS, (TX == DT_F16 ? 10 : 7)>(wv[r], pr);
-            else
-                unit_pairs_bf16_u8(wv[r], pr);
-            const float s0 = kMagic ? sc[r][0] * kPow : sc[r][0];
-            const float s1 = kMagic ? sc[r][1] * kPow : sc[r][1];
-            const float c0 = kMagic ? fmaf(-sc[r][0], kPow, bi[r][0]) : bi[r][0];
-            const float c1 = kMagic ? fmaf(-sc[r][1], kPow, bi[r][1]) : bi[r][1];
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) d0 = dot2(xp[m][i], pr[i], d0, TX);
-#pragma unroll
-                for (int i = 16; i < 32; i++) d1 = dot2(xp[m][i], pr[i], d1, TX);
-                acc[r][m] = (s0 * d0 + c0 * h0[m]) + (s1 * d1 + c1 * h1[m]);
+            const uint16_t* ps = reinterpret_cast<const uint16_t*>(ls + r * sb_row);
+            const uint16_t* pb = reinterpret_cast<const uint16_t*>(lb + r * sb_row);
+            s0 = SB == DT_F16 ? f16_to_f32(ps[0]) : bf16_to_f32(ps[0]);
+            b0 = SB == DT_F16 ? f16_to_f32(pb[0]) : bf16_to_f32(pb[0]);
+            if constexpr (TWO) {
+                s1 = SB == DT_F16 ? f16_to_f32(ps[1]) : bf16_to_f32(ps[1]);
+                b1 = SB == DT_F16 ? f16_to_f32(pb[1]) : bf16_to_f32(pb[1]);
             }
         }
-        if (!active) {
 #pragma unroll
-            for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
-        }
+        for (int m = 0; m < MR; m++) acc[r * MR + m] = row_partial<BITS, TX, OP, TWO>(w[r], xo[m], s0, b0, s1, b1);
+    }
+    // idle lanes (K < 4096) hold zero codes and x; zero them outright so a
+    // non-finite scale they read cannot leak into the sums
+    if (units < 64) {
+#pragma unroll
+        for (int i = 0; i < V; i++) acc[i] = active ? acc[i] : 0.f;
     }
 
-    // ---- reduce across the wave; lane r*MR+m stores (row r, x row m) ----
+    // ---- 6. reduce 8 values at a time; lanes with (lane & 7) == 0 store ----
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            const float v = wave_sum(acc[r][m]);
-            if (lane == r * MR + m && m < M && n0 + r < N) store_f(y, (size_t)m * N + n0 + r, out_dt, v);
-        }
+    for (int c = 0; c < VP / 8; c++) {
+        const float z = sum8(acc + 8 * c, lane) * out_scale<OP>();
+        const int v = 8 * c + sum8_index(lane);
+        const int r = v / MR, m = v % MR;
+        if ((lane & 7) == 0 && v < V && m < M && n0 + r < N) store_f(y, (size_t)m * N + n0 + r, out_dt, z);
     }
 }
 
 template <int BITS, int TX, int SB, int MR, int R>
-LuxStatus launch_reg(const QmmArgs& a, hipStream_t st) {
-    const int waves = (a.N + R - 1) / R;
-    const int blocks = (waves + 3) / 4;
-    hipLaunchKernelGGL((qgemv_reg_kernel<BITS, TX, SB, MR, R>), dim3(blocks), dim3(kThreads), 0, st,
-                       a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K, a.N, a.group_size, a.out_dtype);
+LuxStatus launch_stream(const QmmArgs& a, hipStream_t st) {
+    const int rows = kStreamWaves * R;
+    const int blocks = (a.N + rows - 1) / rows;
+    const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
+    if (a.group_size == 32)
+        hipLaunchKernelGGL((qgemv_stream_kernel<BITS, TX, SB, MR, R, true>), dim3(blocks),
+                           dim3(64 * kStreamWaves), 0, st, a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K,
+                           a.N, gshift, a.out_dtype);
+    else
+        hipLaunchKernelGGL((qgemv_stream_kernel<BITS, TX, SB, MR, R, false>), dim3(blocks),
+                           dim3(64 * kStreamWaves), 0, st, a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K,
+                           a.N, gshift, a.out_dtype);
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 
-// rows per wave: keep the in-flight weight words per lane near 64
+// rows per wave: the block's 4R rows times about two blocks per CU cover N
+// for the large shapes; fewer rows with more x rows in registers
 template <int BITS, int TX, int MR>
-LuxStatus launch_reg_r(const QmmArgs& a, hipStream_t st) {
-    constexpr int R = (MR >= 4) ? 4 : (BITS <= 4 ? 8 : 4);
+LuxStatus launch_stream_r(const QmmArgs& a, hipStream_t st) {
+    constexpr int R = (MR >= 4 || TX == DT_F32) ? 4 : 7;
     switch (a.sb_dtype) {
-    case DT_F32: return launch_reg<BITS, TX, DT_F32, MR, R>(a, st);
-    case DT_F16: return launch_reg<BITS, TX, DT_F16, MR, R>(a, st);
-    default: return launch_reg<BITS, TX, DT_BF16, MR, R>(a, st);
+    case DT_F32: return launch_stream<BITS, TX, DT_F32, MR, R>(a, st);
+    case DT_F16: return launch_stream<BITS, TX, DT_F16, MR, R>(a, st);
+    default: return launch_stream<BITS, TX, DT_BF16, MR, R>(a, st);
     }
 }
 
@@ -443,9 +653,11 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
 template <int BITS, int TX>
 LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
     if (a.K <= 4096 && (a.M <= 4 && (TX != DT_F32 || a.M == 1))) {
-        if (a.M <= 1) return launch_reg_r<BITS, TX, 1>(a, st);
-        if (a.M <= 2) return launch_reg_r<BITS, TX, 2>(a, st);
-        return launch_reg_r<BITS, TX, 4>(a, st);
+        if (a.M <= 1) return launch_stream_r<BITS, TX, 1>(a, st);
+        if constexpr (TX != DT_F32) {
+            if (a.M <= 2) return launch_stream_r<BITS, TX, 2>(a, st);
+            return launch_stream_r<BITS, TX, 4>(a, st);
+        }
     }
     if (a.M <= 1) return launch_t<BITS, TX, 1>(a, st);
     if (a.M <= 2) return launch_t<BITS, TX, 2>(a, st);
