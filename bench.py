@@ -228,6 +228,41 @@ def profiled_traffic(path):
     return None
 
 
+# (name, M, K, N, bits, group, x dtype, scale dtype, out dtype)
+SWEEP = [
+    ("c0", 1, 4096, 4096, 4, 64, F32, F32, F32),
+    ("c1", 1, 4096, 14336, 4, 64, F16, F16, F16),
+    ("c1", 4, 4096, 14336, 4, 64, F16, F16, F16),
+    ("c1", 8, 4096, 14336, 4, 64, F16, F16, F16),
+    ("c2", 32, 8192, 8192, 8, 128, BF16, BF16, BF16),
+    ("c3", 2048, 4096, 4096, 4, 64, BF16, BF16, BF16),
+    ("c3", 2048, 4096, 14336, 4, 64, BF16, BF16, BF16),
+    ("c4", 1, 4096, 11008, 3, 64, F16, F16, F16),
+    ("c4", 1, 4096, 11008, 6, 64, F16, F16, F16),
+    ("c4", 64, 4096, 11008, 3, 64, F16, F16, F16),
+    ("c4", 64, 4096, 11008, 6, 64, F16, F16, F16),
+]
+
+
+def sweep(ctx, hip, steps):
+    """One line per config: kernel AUTO picks, graph-replay time per launch,
+    weight GB/s and TFLOP/s with their roofline fractions."""
+    from mlx_amd import abi
+    names = {abi.KERNEL_GEMV: "gemv", abi.KERNEL_GEMM: "gemm"}
+    for name, M, K, N, bits, gs, xd, sbd, od in SWEEP:
+        kern = ctx.select_kernel(M, K, N, gs, bits, xd, sbd)
+        copies = 4 if M >= 256 else 16
+        r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, 8, abi.KERNEL_AUTO, copies=copies)
+        t = r["kernel_ms_avg"] * 1e-3
+        wb = weight_bytes(N, K, bits, gs, sbd)
+        flops = 2.0 * M * N * K
+        print(json.dumps({"config": name, "M": M, "K": K, "N": N, "bits": bits, "group_size": gs,
+                          "kernel": names.get(kern, str(kern)), "us": round(t * 1e6, 3),
+                          "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
+                          "tflops": round(flops / t / 1e12, 2),
+                          "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -235,6 +270,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the headline line, one JSON line per BASELINE config")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a device-to-device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -250,6 +287,10 @@ def main():
     from mlx_amd import abi, runtime
     hip = Hip()
     ctx = runtime.Context(0)
+    if args.sweep:
+        sweep(ctx, hip, min(args.steps, 256))
+        ctx.close()
+        return
 
     M, K, N, bits, gs = 1, 4096, 14336, 4, 64
     r = bench_qmm(ctx, hip, M, K, N, bits, gs, F16, F16, F16, args.steps, args.warmup,

@@ -28,6 +28,9 @@ struct QmmArgs {
 
 // bandwidth-bound dequant-GEMV (any M; tuned for M <= 8); needs K % 64 == 0
 LuxStatus launch_qgemv(const QmmArgs& a, hipStream_t st);
+// MFMA kernel for 2 <= M <= 16, 4/8-bit codes, f16/bf16 x; NotSupported
+// for other shapes (launch_qgemv tries it first)
+LuxStatus launch_qmm_skinny(const QmmArgs& a, hipStream_t st);
 // MFMA GEMM for f16/bf16 activations; needs K % 64 == 0
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st);
 // generic one-thread-per-output kernel for shapes the tiled kernels reject

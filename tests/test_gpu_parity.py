@@ -90,6 +90,20 @@ def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"gemv b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
+    """5 <= M <= 16 with 4/8-bit codes runs the MFMA small-M kernel: every
+    group size, 8/16/32 groups per wave, row tails inside a 16-row tile."""
+    O = oracle
+    for (M, K, N, gs) in [(5, 1024, 77, 32), (8, 2048, 50, 64), (16, 4096, 40, 128),
+                          (6, 4096, 33, 64), (12, 4096, 21, 32)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 7 + M)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"small-M b{bits} M{M} K{K} N{N} g{gs}")
+
+
 def test_gemv_is_deterministic(ctx, oracle):
     O = oracle
     x, w_q, s, b, _ = O.make_problem(4, 4096, 512, 4, 64, F16, F16, seed=5)
