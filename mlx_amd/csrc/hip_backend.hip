@@ -265,15 +265,21 @@ int gemv_max_m() {
     return v;
 }
 
-// shapes the MFMA GEMM takes: 16-bit activations, K a multiple of 256 (its
-// scale windows span 4 K steps of 64), x and W below 4 GiB (32-bit offsets),
-// and its LDS buffers within one CU's 160 KB (f32 scales at group size 32
-// with 6- or 8-bit codes do not fit)
+// shapes the MFMA GEMMs take: 16-bit activations, and
+//  * 8 < M <= 64 with K a multiple of 1024 (small-M kernel: its 4 waves split
+//    K into parts of 4-step multiples), x and W below 2 GiB; or
+//  * K a multiple of 256 (the large kernel's scale windows span 4 K steps of
+//    64), x and W below 4 GiB (32-bit offsets), and its LDS buffers within
+//    one CU's 160 KB (f32 scales at group size 32 with 6- or 8-bit codes do
+//    not fit)
 bool gemm_ok(int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dtype,
              LuxBackendDtype sb_dtype) {
+    if (x_dtype == LUX_DTYPE_FLOAT32) return false;
+    if (M > 8 && M <= 64 && K % 1024 == 0 && (size_t)M * K * 2 < (1ull << 31) &&
+        (size_t)N * K * bits / 8 < (1ull << 31))
+        return true;
     if (sb_dtype == LUX_DTYPE_FLOAT32 && group_size == 32 && bits >= 6) return false;
-    return x_dtype != LUX_DTYPE_FLOAT32 && K % 256 == 0 &&
-           (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
+    return K % 256 == 0 && (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
 }
 
 LuxQuantKernel select_kernel_impl(int M, int K, int N, int group_size, int bits,

@@ -5,6 +5,11 @@
 namespace lxq {
 
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st) {
+    // 8 < M <= 64: the W-streaming small-M kernel where it applies
+    if (a.M <= 64) {
+        const LuxStatus s = launch_qgemm_small(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     // the scale windows cover 4 K steps of 64 codes
     if (a.K % 256 != 0) return LuxStatus::NotSupported;
     // x and W offsets are 32-bit: each must stay below 4 GiB

@@ -1,0 +1,323 @@
+// qgemm_small.h -- MFMA GEMM for 8 < M <= 64 (gfx950): the GEMM semantics
+// (weights dequantized to the activation type T, fp32 accumulation) with W
+// streamed once from HBM.
+//
+// A block owns 32 columns n (rows of W) and all of M; its 4 waves split K
+// in four parts and meet in LDS at the end (no barrier in the main loop).
+// v_mfma_f32_32x32x16_{bf16,f16}: A = x (rows m = lane % 32 of an M tile),
+// B = W (column n = lane % 32).  Lane half h = lane / 32 owns the 32 codes
+// [64q + 32h, +32) of step q; sub-step s takes codes 32h + 8s .. +8 from both
+// halves, so a lane's codes of a step are one contiguous 4*BITS-byte slice,
+// dequantized to T (RNE of fmaf(s, q, b)) in registers, and its x operand is
+// the matching 16 bytes of row m.
+//
+// Operands reach the MFMA through LDS, each wave in its own rings (no
+// barriers): a fragment load straight from global memory would touch 32
+// rows = 32 cache lines per instruction, while a buffer->LDS DMA of 1 KB
+// covers 8 lines.  x: one step (MT*32 rows x 128 B) per slot, 16-byte chunks
+// XOR-swizzled by row through the DMA source address (conflict-free fragment
+// reads); W and scales/biases: four steps per slot.  Each wave waits on a
+// compile-time count of its own outstanding DMAs once per step.
+#pragma once
+#include "kernels.h"
+#include "qcommon.h"
+
+namespace lxq {
+namespace small {
+
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 4;
+
+template <int TX>
+__device__ __forceinline__ f32x16 mfma(const u4& a, const u4& b, const f32x16& c) {
+    if constexpr (TX == DT_BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                     0, 0, 0);
+}
+
+// wait until at most N vector-memory instructions of this wave are in flight
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_small() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int SB>
+__device__ __forceinline__ float sb_val(uint32_t w) {
+    if constexpr (SB == DT_F32) return __uint_as_float(w);
+    else if constexpr (SB == DT_F16) return f16_to_f32(w & 0xffffu);
+    else return bf16_to_f32(w & 0xffffu);
+}
+// two fp32 values -> a packed pair of T, RNE, as one packed conversion: a
+// scalar (_Float16) cast of an fmaf result lets the compiler fuse both into
+// v_fma_mixlo_f16, which rounds once (exact -> f16) where the format rounds
+// twice (exact -> fp32 -> f16) and differs at f16 ties
+template <int TX>
+__device__ __forceinline__ uint32_t pack_t(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    if constexpr (TX == DT_BF16) {
+        typedef __bf16 t2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, t2));
+    } else {
+        typedef _Float16 t2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, t2));
+    }
+}
+
+// codes 8s .. 8s+7 of the lane's 32 (held in BITS words) dequantized to T:
+// the B operand of sub-step s
+template <int BITS, int TX>
+__device__ __forceinline__ u4 w_operand(const uint32_t* c, float sc, float bi, int s) {
+    float q[8];
+    if constexpr (BITS == 4) {
+        const uint32_t w = c[s], lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            q[2 * e] = (float)((lo >> (8 * e)) & 0xffu);
+            q[2 * e + 1] = (float)((hi >> (8 * e)) & 0xffu);
+        }
+    } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) q[e] = (float)((c[2 * s + (e >> 2)] >> (8 * (e & 3))) & 0xffu);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) q[e] = (float)unit_code<BITS>(c, 8 * s + e);
+    }
+    u4 r;
+    r.x = pack_t<TX>(fmaf(sc, q[0], bi), fmaf(sc, q[1], bi));
+    r.y = pack_t<TX>(fmaf(sc, q[2], bi), fmaf(sc, q[3], bi));
+    r.z = pack_t<TX>(fmaf(sc, q[4], bi), fmaf(sc, q[5], bi));
+    r.w = pack_t<TX>(fmaf(sc, q[6], bi), fmaf(sc, q[7], bi));
+    return r;
+}
+
+// buffer->LDS DMA, lane l copies E bytes to LDS address m0 + E l (global
+// address = SGPR base + 32-bit lane offset; every offset here is in bounds)
+__device__ __forceinline__ void dma16(uint32_t m0v, const void* sbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" : : "s"(m0v), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t m0v, const void* sbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" : : "s"(m0v), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <int BITS, int SB, int MT, int GS>
+struct Lay {
+    static constexpr int kSb = SB == DT_F32 ? 4 : 2;
+    static constexpr int kXS = MT * 32 * 128;           // one x step
+    static constexpr int kRX = MT == 1 ? 3 : 2;         // x steps resident (one being read)
+    static constexpr int kWS = 32 * 32 * BITS;          // one W super-step (4 steps)
+    static constexpr int kSPR = (256 / GS) * kSb;       // scale bytes per row per super-step
+    static constexpr int kDpr = kSPR / 4;               // ... in dwords (1..8)
+    static constexpr int kNS = (32 * kDpr + 63) / 64;   // DMAs per scale super-step
+    static constexpr int kSS = 32 * kSPR;
+    static constexpr int kNX = 4 * MT;                  // x DMAs per step
+    static constexpr int kNWS = BITS + 2 * kNS;         // W + scale + bias DMAs per super-step
+    // loads younger than X(q) when step q waits: the x and W DMAs issued in
+    // steps q - kRX + 2 .. q, at most (kRX - 1) x-issues and one W issue
+    static constexpr int kMaxWait = (kRX - 1) * kNX + kNWS;
+    // W super-steps resident: 3 (two in flight) unless LDS or vmcnt say 2
+    static constexpr int kWaveBytes3 = kRX * kXS + 3 * (kWS + 2 * kSS);
+    static constexpr int kRW = (4 * kWaveBytes3 <= 160 * 1024) ? 3 : 2;
+    static constexpr int kX0 = 0, kW0 = kRX * kXS, kS0 = kW0 + kRW * kWS, kB0 = kS0 + kRW * kSS;
+    static constexpr int kWaveBytes = kB0 + kRW * kSS;
+    static constexpr int kRed = 4 * MT * 16 * 64 * 4;   // final K-part reduction (reuses the rings)
+    static constexpr int kBytes = (4 * kWaveBytes > kRed) ? 4 * kWaveBytes : kRed;
+    static_assert(kMaxWait < 64, "vmcnt holds 6 bits");
+    static_assert(kSPR % 4 == 0, "scale rows of a super-step are whole dwords");
+};
+
+template <int BITS, int SB, int MT, int GS>
+struct Ctx {
+    uint32_t lds;                 // LDS address of this wave's rings
+    const uint8_t* x;             // x + this wave's first k (bytes)
+    const uint8_t* w;             // w_q + this wave's first code (bytes)
+    const uint8_t* s;             // scales + this wave's first group (bytes)
+    const uint8_t* b;
+    uint32_t xoff[4 * MT];        // per x DMA: row (clamped) and swizzled chunk
+    uint32_t woff[BITS];          // per W DMA: row (clamped) and chunk
+    uint32_t soff[Lay<BITS, SB, MT, GS>::kNS];
+    bool sact[Lay<BITS, SB, MT, GS>::kNS];
+};
+
+template <int BITS, int SB, int MT, int GS>
+__device__ __forceinline__ void issue_x(const Ctx<BITS, SB, MT, GS>& c, int qs) {  // qs: step within the part
+    using L = Lay<BITS, SB, MT, GS>;
+    const uint32_t base = c.lds + L::kX0 + (uint32_t)(qs % L::kRX) * L::kXS;
+    const uint8_t* src = c.x + (size_t)qs * 128;
+#pragma unroll
+    for (int i = 0; i < L::kNX; i++) dma16(base + 1024u * i, src, c.xoff[i]);
+}
+template <int BITS, int SB, int MT, int GS>
+__device__ __forceinline__ void issue_w(const Ctx<BITS, SB, MT, GS>& c, int u) {  // u: super-step within the part
+    using L = Lay<BITS, SB, MT, GS>;
+    const uint32_t slot = (uint32_t)(u % L::kRW);
+    const uint8_t* src = c.w + (size_t)u * 32 * BITS;
+#pragma unroll
+    for (int i = 0; i < BITS; i++) dma16(c.lds + L::kW0 + slot * L::kWS + 1024u * i, src, c.woff[i]);
+    const uint8_t* ss = c.s + (size_t)u * L::kSPR;
+    const uint8_t* bs = c.b + (size_t)u * L::kSPR;
+#pragma unroll
+    for (int i = 0; i < L::kNS; i++) {
+        if (c.sact[i]) dma4(c.lds + L::kS0 + slot * L::kSS + 256u * i, ss, c.soff[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < L::kNS; i++) {
+        if (c.sact[i]) dma4(c.lds + L::kB0 + slot * L::kSS + 256u * i, bs, c.soff[i]);
+    }
+}
+
+// step q (P = q % 4, compile time) of a wave whose part has nq steps
+template <int BITS, int TX, int SB, int MT, int GS, int P>
+__device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, GS>& c, uint8_t* lw, int q,
+                                     int nq) {
+    using L = Lay<BITS, SB, MT, GS>;
+    const int u = q >> 2;
+    // issue: W/scales of super-step u + kRW - 1 (at P == 0), x of step q + kRX - 1
+    // (past the part's end they repeat its last super-step / step: counts stay fixed)
+    if constexpr (P == 0) {
+        const int uw = u + L::kRW - 1, ul = (nq >> 2) - 1;
+        issue_w(c, uw < ul ? uw : ul);
+    }
+    {
+        const int qx = q + L::kRX - 1;
+        issue_x(c, qx < nq ? qx : nq - 1);
+    }
+    // X(q) (and the older W(u)) landed: younger are the issues of steps
+    // q - kRX + 2 .. q: kRX - 1 x issues, plus a W issue for each of those
+    // steps that starts a super-step
+    constexpr int kYoung = (L::kRX - 1) * L::kNX + L::kNWS * (((P == 0) ? 1 : 0) + ((L::kRX == 3 && P == 1) ? 1 : 0));
+    wait_vmcnt_small<kYoung>();
+    const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+    // x fragments
+    const uint8_t* xs = lw + L::kX0 + (q % L::kRX) * L::kXS;
+    u4 xf[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int r = 32 * t + j;
+#pragma unroll
+        for (int s = 0; s < 4; s++) xf[t][s] = *reinterpret_cast<const u4*>(xs + r * 128 + (((4 * h + s) ^ swz(r)) * 16));
+    }
+    // codes and scale of this lane's 32 codes
+    const int slot = u % L::kRW;
+    const uint32_t* wc = reinterpret_cast<const uint32_t*>(lw + L::kW0 + slot * L::kWS + j * 32 * BITS + P * 8 * BITS + 4 * BITS * h);
+    uint32_t cw[BITS];
+#pragma unroll
+    for (int i = 0; i < BITS; i++) cw[i] = wc[i];
+    const int gi = (P * 64 + 32 * h) / GS;
+    const uint8_t* sp = lw + L::kS0 + slot * L::kSS + j * L::kSPR + gi * L::kSb;
+    const uint8_t* bp = lw + L::kB0 + slot * L::kSS + j * L::kSPR + gi * L::kSb;
+    float sc, bi;
+    if constexpr (SB == DT_F32) { sc = *reinterpret_cast<const float*>(sp); bi = *reinterpret_cast<const float*>(bp); }
+    else if constexpr (SB == DT_F16) { sc = f16_to_f32(*reinterpret_cast<const uint16_t*>(sp)); bi = f16_to_f32(*reinterpret_cast<const uint16_t*>(bp)); }
+    else { sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(sp)); bi = bf16_to_f32(*reinterpret_cast<const uint16_t*>(bp)); }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const u4 wop = w_operand<BITS, TX>(cw, sc, bi, s);
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc[t] = mfma<TX>(xf[t][s], wop, acc[t]);
+    }
+}
+
+template <int BITS, int TX, int SB, int MT, int GS>
+__global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
+    const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int out_dt) {
+    using L = Lay<BITS, SB, MT, GS>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.x * 32;
+    const int G = K / GS;
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+    const int nq = K / 64 / kWaves;        // steps of this wave's K part (a multiple of 4)
+    const int k0 = wave * nq * 64;         // first k of the part
+
+    Ctx<BITS, SB, MT, GS> c;
+    c.lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds) + (uint32_t)wave * L::kWaveBytes;
+    c.x = static_cast<const uint8_t*>(x) + (size_t)k0 * 2;
+    c.w = reinterpret_cast<const uint8_t*>(wq) + (size_t)k0 * BITS / 8;
+    c.s = static_cast<const uint8_t*>(scales) + (size_t)(k0 / GS) * L::kSb;
+    c.b = static_cast<const uint8_t*>(biases) + (size_t)(k0 / GS) * L::kSb;
+#pragma unroll
+    for (int i = 0; i < L::kNX; i++) {
+        const int r = 8 * i + (lane >> 3);                       // row within the MT*32 rows
+        const int m = r < M ? r : M - 1;
+        const int chunk = (lane & 7) ^ swz(r);                   // global chunk landing in slot lane & 7
+        c.xoff[i] = ((uint32_t)m * K + 8 * chunk) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < BITS; i++) {
+        const int v = 64 * i + lane, r = v / (2 * BITS), ch = v % (2 * BITS);
+        const int n = n0 + r < N ? n0 + r : N - 1;
+        c.woff[i] = (uint32_t)n * row_bytes + 16u * ch;
+    }
+#pragma unroll
+    for (int i = 0; i < L::kNS; i++) {
+        const int v = 64 * i + lane, r = v / L::kDpr, d = v % L::kDpr;
+        const int n = n0 + r < N ? n0 + r : N - 1;
+        c.sact[i] = v < 32 * L::kDpr;
+        c.soff[i] = (uint32_t)n * G * L::kSb + 4u * d;
+    }
+    uint8_t* lw = lds + (size_t)wave * L::kWaveBytes;
+
+    // prologue: the issues of steps -kRX+1 .. -1 and super-steps up to kRW - 2
+    // in the same order the steady state keeps (missing ones repeat step 0)
+#pragma unroll
+    for (int uu = 0; uu < L::kRW - 1; uu++) issue_w(c, uu < (nq >> 2) - 1 ? uu : (nq >> 2) - 1);
+#pragma unroll
+    for (int qq = 0; qq < L::kRX - 1; qq++) issue_x(c, qq < nq - 1 ? qq : nq - 1);
+    // the steady state's W issue of super-step kRW - 1 happens in step 0
+
+    f32x16 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
+    for (int q = 0; q < nq; q += 4) {
+        step<BITS, TX, SB, MT, GS, 0>(acc, c, lw, q, nq);
+        step<BITS, TX, SB, MT, GS, 1>(acc, c, lw, q + 1, nq);
+        step<BITS, TX, SB, MT, GS, 2>(acc, c, lw, q + 2, nq);
+        step<BITS, TX, SB, MT, GS, 3>(acc, c, lw, q + 3, nq);
+    }
+    wait_vmcnt_small<0>();
+    __syncthreads();
+
+    // ---- the four K parts meet in LDS; wave w stores accumulator VGPRs 4w..4w+3 ----
+    float* red = reinterpret_cast<float*>(lds);   // [wave][MT*16][64]
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) red[((size_t)wave * MT * 16 + t * 16 + v) * 64 + lane] = acc[t][v];
+    __syncthreads();
+    const int nn = n0 + j;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            const int v = 4 * wave + vv;
+            float sum = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < kWaves; w2++) sum += red[((size_t)w2 * MT * 16 + t * 16 + v) * 64 + lane];
+            // 32x32 accumulator layout: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
+            const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m < M && nn < N) store_f(y, (size_t)m * N + nn, out_dt, sum);
+        }
+}
+
+}  // namespace small
+
+// launcher (qgemm_small.hip): NotSupported unless 8 < M <= 64, f16/bf16 x, K % 1024 == 0
+LuxStatus launch_qgemm_small(const QmmArgs& a, hipStream_t st);
+
+}  // namespace lxq

@@ -253,6 +253,21 @@ def test_gemm_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"gemm b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_small_gemm_parity(ctx, oracle, bits, xd, sbd, od):
+    """8 < M <= 64 with K % 1024 == 0 runs the W-streaming small-M GEMM: the
+    same "dequantize to T, then matmul" form as the large GEMM, one and two
+    32-row M tiles, ragged M and N, every group size, 4/8/12 steps per wave."""
+    O = oracle
+    for (M, K, N, gs) in [(9, 1024, 77, 64), (32, 2048, 130, 128), (33, 1024, 40, 32),
+                          (64, 1024, 96, 64), (48, 3072, 33, 32)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 13 + M)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, w_round=xd)
+        check_output(O, y, want, od, f"small gemm b{bits} M{M} K{K} N{N} g{gs}")
+
+
 def test_gemm_shape_limits(ctx, oracle):
     """K not a multiple of 256: an explicit GEMM request is NOT_SUPPORTED,
     AUTO picks the GEMV (exact weights) for any M."""
