@@ -13,8 +13,12 @@ size_t gemv_lds_bytes(int MR, int K, int x_dtype) {
 // fits in 64 KB of LDS (two blocks per CU).
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
-    // 5..16 rows of x: the MFMA kernel where it applies (4/8-bit, 16-bit x);
-    // up to 4 rows the streaming kernel keeps x in registers and is as fast
+    // 2..16 rows of x: the MFMA kernels where they apply (4/8-bit, 16-bit x;
+    // the LDS-ring kernel needs K % 1024 == 0)
+    if (args.M >= 2 && args.M <= 16) {
+        const LuxStatus s = launch_qgemv_mid(args, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     if (args.M >= 5 && args.M <= 16) {
         const LuxStatus s = launch_qmm_skinny(args, st);
         if (s != LuxStatus::NotSupported) return s;

@@ -93,11 +93,13 @@ def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
-    """5 <= M <= 16 with 4/8-bit codes runs the MFMA small-M kernel: every
-    group size, 8/16/32 groups per wave, row tails inside a 16-row tile."""
+    """2 <= M <= 16 with 4/8-bit codes runs an MFMA kernel (the LDS-ring one
+    for K % 1024 == 0, else the skinny one): every group size, one and two
+    x DMAs per step, row tails in the 16-row tile and in the 32-column block."""
     O = oracle
-    for (M, K, N, gs) in [(5, 1024, 77, 32), (8, 2048, 50, 64), (16, 4096, 40, 128),
-                          (6, 4096, 33, 64), (12, 4096, 21, 32)]:
+    for (M, K, N, gs) in [(2, 1024, 77, 32), (4, 2048, 50, 64), (5, 1024, 77, 32), (8, 2048, 50, 64),
+                          (16, 4096, 40, 128), (6, 4096, 33, 64), (12, 4096, 21, 32), (3, 3072, 65, 128),
+                          (9, 1024, 96, 64), (7, 512, 40, 64), (10, 256, 19, 32)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 7 + M)
         y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
