@@ -234,6 +234,16 @@ constexpr uint32_t kZeroOff = 0x80000000u;
 
 constexpr int kStreamWaves = 4;
 
+// Staged x of the stream kernel: unit u (64 elements, 8 or 16 chunks of 16 B)
+// keeps logical chunk j in slot j ^ x_swz(u).  Lane u reads its own unit, so
+// the lanes of one LDS pass read units 128 or 256 B apart; the swizzle puts
+// them in different bank groups (16 consecutive lanes hit 16 distinct 16-byte
+// slots of a 256-byte window).
+template <int XE>
+__device__ __host__ __forceinline__ int x_swz(int u) {
+    return XE == 4 ? (u & 15) : ((u & 7) ^ ((u >> 3) & 1));
+}
+
 enum : int { OP_SUB4 = 0, OP_SUB8 = 1, OP_MAGIC = 2, OP_BF16U8 = 3, OP_F32 = 4 };
 template <int BITS, int TX>
 constexpr int op_kind() {
@@ -286,12 +296,13 @@ struct XOps {
 };
 
 template <int BITS, int TX, int OP>
-__device__ __forceinline__ void prep_x(const uint8_t* lx, XOps<BITS, TX, OP>& o) {
+__device__ __forceinline__ void prep_x(const uint8_t* lx, int sw, XOps<BITS, TX, OP>& o) {
+    // lx: the lane's staged unit, logical chunk i in slot i ^ sw (x_swz)
     if constexpr (OP == OP_F32) {
         const v4u32* p = reinterpret_cast<const v4u32*>(lx);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const v4u32 t = p[i];
+            const v4u32 t = p[i ^ sw];
             o.v[4 * i] = t.x; o.v[4 * i + 1] = t.y; o.v[4 * i + 2] = t.z; o.v[4 * i + 3] = t.w;
         }
         float a = 0.f, b = 0.f;
@@ -307,7 +318,7 @@ __device__ __forceinline__ void prep_x(const uint8_t* lx, XOps<BITS, TX, OP>& o)
         const v4u32* p = reinterpret_cast<const v4u32*>(lx);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const v4u32 t = p[i];
+            const v4u32 t = p[i ^ sw];
             nat[4 * i] = t.x; nat[4 * i + 1] = t.y; nat[4 * i + 2] = t.z; nat[4 * i + 3] = t.w;
         }
         // half sums: dot2 against (1, 1) is exact per product, fp32 accumulate
@@ -500,7 +511,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
         for (int c0 = 0; c0 < XC; c0 += 64 * kStreamWaves) {
             const int cw = c0 + wave * 64, c = cw + lane;
             const int m = c / (L::kXRow / 16), cc = c % (L::kXRow / 16);
-            const uint32_t voff = (cc < kc && m < M) ? (uint32_t)(m * K * XE + cc * 16) : kZeroOff;
+            // LDS slot cc holds the unit's chunk (cc % CPU) ^ swz, read back by prep_x
+            constexpr int CPU = 4 * XE;  // 16-byte chunks per 64-element unit
+            const int xu = cc / CPU, src = xu * CPU + ((cc % CPU) ^ x_swz<XE>(xu));
+            const uint32_t voff = (cc < kc && m < M) ? (uint32_t)(m * K * XE + src * 16) : kZeroOff;
             if (cw < XC)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(lds + L::X + cw * 16), 16, voff, 0, 0, 0);
         }
@@ -544,7 +558,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
     // ---- 4. x operands ----
     XOps<BITS, TX, OP> xo[MR];
 #pragma unroll
-    for (int m = 0; m < MR; m++) prep_x<BITS, TX, OP>(lds + L::X + m * L::kXRow + u * 64 * XE, xo[m]);
+    for (int m = 0; m < MR; m++) prep_x<BITS, TX, OP>(lds + L::X + m * L::kXRow + u * 64 * XE, x_swz<XE>(u), xo[m]);
 
     // ---- 5. rows in arrival order ----
     // the unit's first group (codes 64u..): group size 32 -> 2u (and 2u+1)
