@@ -31,6 +31,9 @@ LuxStatus launch_qgemv(const QmmArgs& a, hipStream_t st);
 // MFMA kernel for 2 <= M <= 16, 4/8-bit codes, f16/bf16 x; NotSupported
 // for other shapes (launch_qgemv tries it first)
 LuxStatus launch_qmm_skinny(const QmmArgs& a, hipStream_t st);
+// MFMA decode kernel for 2 <= M <= 8, 4-bit codes, f16/bf16 x, K % 1024 == 0,
+// K <= 8192; NotSupported otherwise (tried first)
+LuxStatus launch_qgemv_dec(const QmmArgs& a, hipStream_t st);
 // MFMA kernel with LDS operand rings for 2 <= M <= 16, 4/8-bit codes,
 // f16/bf16 x, K % 1024 == 0; NotSupported otherwise (tried before the above)
 LuxStatus launch_qgemv_mid(const QmmArgs& a, hipStream_t st);

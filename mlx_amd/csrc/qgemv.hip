@@ -13,8 +13,13 @@ size_t gemv_lds_bytes(int MR, int K, int x_dtype) {
 // fits in 64 KB of LDS (two blocks per CU).
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
-    // 2..16 rows of x: the MFMA kernels where they apply (4/8-bit, 16-bit x;
-    // the LDS-ring kernel needs K % 1024 == 0)
+    // 2..16 rows of x: the MFMA kernels where they apply (16-bit x; the
+    // decode kernel takes 4-bit codes and M <= 8, the LDS-ring kernel 4/8-bit
+    // codes; both need K % 1024 == 0)
+    if (args.M >= 2 && args.M <= 8) {
+        const LuxStatus s = launch_qgemv_dec(args, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     if (args.M >= 2 && args.M <= 16) {
         const LuxStatus s = launch_qgemv_mid(args, st);
         if (s != LuxStatus::NotSupported) return s;
