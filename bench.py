@@ -263,6 +263,19 @@ def sweep(ctx, hip, steps):
                           "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4)}), flush=True)
 
 
+def decode_legs(ctx, hip, K, N, bits, gs, steps):
+    """configs[1] at M=4 and M=8: same weight bytes as M=1, 4x / 8x the math."""
+    from mlx_amd import abi
+    out = {}
+    wb = weight_bytes(N, K, bits, gs, F16)
+    for m in (4, 8):
+        r = bench_qmm(ctx, hip, m, K, N, bits, gs, F16, F16, F16, min(steps, 1024), 16, abi.KERNEL_AUTO)
+        t = r["kernel_ms_avg"] * 1e-3
+        out[f"M{m}"] = {"kernel_us_avg": round(t * 1e6, 3), "weight_GBs": round(wb / t / 1e9, 1),
+                        "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,6 +285,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE config")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the configs[1] M=4 and M=8 decode legs (for profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a device-to-device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -293,6 +308,10 @@ def main():
         return
 
     M, K, N, bits, gs = 1, 4096, 14336, 4, 64
+    if args.decode_only:
+        print(json.dumps({"decode_m4_m8": decode_legs(ctx, hip, K, N, bits, gs, args.steps)}), flush=True)
+        ctx.close()
+        return
     r = bench_qmm(ctx, hip, M, K, N, bits, gs, F16, F16, F16, args.steps, args.warmup,
                   abi.KERNEL_AUTO)
     wb = weight_bytes(N, K, bits, gs, F16)
@@ -321,6 +340,7 @@ def main():
                      "kernel_us_single_launch": round(r["single_ms_avg"] * 1e3, 3),
                      "algorithmic_bytes": wb},
     }
+    line["decode_m4_m8"] = decode_legs(ctx, hip, K, N, bits, gs, args.steps)
     if not args.no_gemm:
         gemm = {}
         for n in (4096, 14336):
