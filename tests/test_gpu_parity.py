@@ -61,18 +61,32 @@ def test_dequantize_bit_exact(ctx, oracle, bits, sb):
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_quantize_bit_exact(ctx, oracle, bits, gs):
+    """Codes, scales and biases bit-equal to the CPU quantizer, for f32 and
+    16-bit weights, a partial last wave (N K / 8 not a multiple of 64), and
+    the cases the parallel min/max must order like the sequential scan: a
+    NaN first weight poisons its group, later NaNs are skipped, ties between
+    -0 and +0 keep the first, an infinite weight."""
     from mlx_amd import runtime
     O = oracle
     N, K = 29, 512
     w = O.rng_normal(N * K, 900 + bits, 0.0, 0.02).reshape(N, K)
     w[0, :gs] = -0.5  # constant group
     w.reshape(-1)[::97] *= 20.0  # outliers
-    for sb in (F32, F16, BF16):
-        print(f"[case] quantize bits={bits} g={gs} sb={sb}", flush=True)
-        gq, gs_, gb = runtime.run_quantize(ctx, w, gs, bits, F32, sb)
-        wq, s, b = O.quantize(w, gs, bits, sb)
-        assert np.array_equal(gq, wq)
-        assert np.array_equal(gs_, s) and np.array_equal(gb, b)
+    w[1, gs] = np.nan             # first weight of group 1: the group is NaN
+    w[1, 2 * gs + 5] = np.nan     # a later weight: skipped
+    w[2, :gs] = 0.0               # mixed-sign zeros: the first occurrence wins
+    w[2, 1:gs:3] = -0.0
+    w[3, 3 * gs + 7] = np.inf
+    for wd in (F32, F16, BF16):
+        wi = w if wd == F32 else O.from_f32(w, wd)
+        wf = w if wd == F32 else O.to_f32(wi, wd)
+        for sb in (F32, F16, BF16):
+            print(f"[case] quantize bits={bits} g={gs} w={wd} sb={sb}", flush=True)
+            gq, gs_, gb = runtime.run_quantize(ctx, wi, gs, bits, wd, sb)
+            wq, s, b = O.quantize(wf, gs, bits, sb)
+            u = np.uint32 if sb == F32 else np.uint16
+            assert np.array_equal(gq, wq)
+            assert np.array_equal(gs_.view(u), s.view(u)) and np.array_equal(gb.view(u), b.view(u))
 
 
 # ---- GEMV ---------------------------------------------------------------
