@@ -67,6 +67,8 @@ BUFFER_COPY_TO_HOST = C.CFUNCTYPE(Err, Ctx, Buf, C.c_void_p, C.c_size_t)
 BUFFER_COPY_FROM_HOST = C.CFUNCTYPE(Err, Ctx, Buf, C.c_void_p, C.c_size_t)
 BUFFER_GET_HOST_PTR = C.CFUNCTYPE(C.c_void_p, Ctx, Buf)
 OP_MATMUL_F32 = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, C.c_int, C.c_int, C.c_int)
+OP_BINARY_F32 = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, C.c_size_t)
+OP_TRANSPOSE_F32 = C.CFUNCTYPE(Err, Ctx, Buf, Buf, C.c_int, C.c_int)
 
 # slot index -> (name, prototype or None).  Slot order is the ABI
 # (backend_plugin.h:82-380; probed offsets in SURVEY Appendix A).
@@ -100,6 +102,11 @@ _PROTOS = {
     "buffer_copy_from_host": BUFFER_COPY_FROM_HOST,
     "buffer_get_host_ptr": BUFFER_GET_HOST_PTR,
     "op_matmul_f32": OP_MATMUL_F32,
+    "op_add_f32": OP_BINARY_F32,
+    "op_sub_f32": OP_BINARY_F32,
+    "op_mul_f32": OP_BINARY_F32,
+    "op_div_f32": OP_BINARY_F32,
+    "op_transpose_f32": OP_TRANSPOSE_F32,
 }
 
 

@@ -398,6 +398,62 @@ LuxBackendError hip_op_quantize(LuxBackendContext* c, LuxBackendBuffer* w, LuxBa
                                            w_dtype, sb_dtype, ctx->stream));
 }
 
+// ---------------------------------------------------------------------------
+// base tensor ops (f32): the slots the reference CPU backend fills
+// (src/cpu_backend.cpp:360-364), plus div and transpose.  Unlike the CPU
+// backend, the element counts are checked against the buffer sizes: a GPU
+// kernel must not read or write past an allocation.
+// ---------------------------------------------------------------------------
+
+bool fits(LuxBackendBuffer* b, size_t floats) { return B(b) && floats <= B(b)->size / 4; }
+
+LuxBackendError elementwise(int op, LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b,
+                            LuxBackendBuffer* out, size_t n) {
+    HipContext* ctx = C(c);
+    if (!ctx || !fits(a, n) || !fits(b, n) || !fits(out, n)) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
+    return map_status(lxq::launch_elementwise(op, static_cast<const float*>(B(a)->ptr),
+                                              static_cast<const float*>(B(b)->ptr), static_cast<float*>(B(out)->ptr),
+                                              n, ctx->stream));
+}
+LuxBackendError hip_op_add_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return elementwise(0, c, a, b, o, n);
+}
+LuxBackendError hip_op_sub_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return elementwise(1, c, a, b, o, n);
+}
+LuxBackendError hip_op_mul_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return elementwise(2, c, a, b, o, n);
+}
+LuxBackendError hip_op_div_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return elementwise(3, c, a, b, o, n);
+}
+
+LuxBackendError hip_op_matmul_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b,
+                                  LuxBackendBuffer* out, int M, int K, int N) {
+    HipContext* ctx = C(c);
+    if (!ctx || M < 0 || K < 0 || N < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (!fits(a, (size_t)M * K) || !fits(b, (size_t)K * N) || !fits(out, (size_t)M * N))
+        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
+    return map_status(lxq::launch_matmul_f32(static_cast<const float*>(B(a)->ptr), static_cast<const float*>(B(b)->ptr),
+                                             static_cast<float*>(B(out)->ptr), M, K, N, ctx->stream));
+}
+
+LuxBackendError hip_op_transpose_f32(LuxBackendContext* c, LuxBackendBuffer* in, LuxBackendBuffer* out, int rows,
+                                     int cols) {
+    HipContext* ctx = C(c);
+    if (!ctx || rows < 0 || cols < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (!fits(in, (size_t)rows * cols) || !fits(out, (size_t)rows * cols)) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
+    return map_status(lxq::launch_transpose_f32(static_cast<const float*>(B(in)->ptr), static_cast<float*>(B(out)->ptr),
+                                                rows, cols, ctx->stream));
+}
+
 void* hip_get_native_stream(LuxBackendContext* c) {
     HipContext* ctx = C(c);
     return ctx ? reinterpret_cast<void*>(ctx->stream) : nullptr;
@@ -426,6 +482,12 @@ lux_gpu_backend_vtbl make_vtbl() {
     v.buffer_copy_to_host = hip_buffer_copy_to_host;
     v.buffer_copy_from_host = hip_buffer_copy_from_host;
     v.buffer_get_host_ptr = hip_buffer_get_host_ptr;
+    v.op_add_f32 = hip_op_add_f32;
+    v.op_sub_f32 = hip_op_sub_f32;
+    v.op_mul_f32 = hip_op_mul_f32;
+    v.op_div_f32 = hip_op_div_f32;
+    v.op_matmul_f32 = hip_op_matmul_f32;
+    v.op_transpose_f32 = hip_op_transpose_f32;
     return v;
 }
 
@@ -459,9 +521,9 @@ extern "C" __attribute__((visibility("default"))) bool lux_gpu_backend_init(lux_
     out->abi_version = LUX_GPU_BACKEND_ABI_VERSION;
     out->backend_name = "hip";
     out->backend_version = "0.1.0";
-    // only buffers and the quantized extension: no base tensor-op slots are
-    // filled, so TENSOR_OPS / MATMUL are not advertised (and never UNIFIED_MEMORY)
-    out->capabilities = 0;
+    // f32 elementwise ops and matmul are filled (never UNIFIED_MEMORY: a
+    // discrete GPU); the quantized ops come through the extension table
+    out->capabilities = LUX_CAP_TENSOR_OPS | LUX_CAP_MATMUL;
     out->vtbl = &g_vtbl;
     return true;
 }

@@ -45,6 +45,13 @@ LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st);
 // generic one-thread-per-output kernel for shapes the tiled kernels reject
 LuxStatus launch_qmm_generic(const QmmArgs& a, hipStream_t st);
 
+// the plugin ABI's f32 tensor ops (base_ops.hip); op: 0 add, 1 sub, 2 mul, 3 div
+LuxStatus launch_elementwise(int op, const float* a, const float* b, float* o, size_t n, hipStream_t st);
+// C[M, N] = A[M, K] . B[K, N], row-major, ascending-k sums without contraction
+LuxStatus launch_matmul_f32(const float* a, const float* b, float* c, int M, int K, int N, hipStream_t st);
+// out[cols, rows] = in[rows, cols]^T
+LuxStatus launch_transpose_f32(const float* in, float* out, int rows, int cols, hipStream_t st);
+
 // out[N, K] = dequant(w_q) in out_dtype
 LuxStatus launch_dequantize(const uint32_t* wq, const void* scales, const void* biases, void* out,
                             int N, int K, int group_size, int bits, int sb_dtype, int out_dtype,

@@ -144,6 +144,19 @@ class Context:
         return self.q.select_kernel(M, K, N, group_size, bits, x_dtype,
                                     x_dtype if sb_dtype is None else sb_dtype)
 
+    # base f32 tensor ops (vtable slots, as the reference core calls them)
+    def binary_f32(self, op: str, a: Buffer, b: Buffer, out: Buffer, n: int) -> None:
+        fn = getattr(self.vt, f"op_{op}_f32")
+        if not fn:
+            raise LuxError(abi.ERR_NOT_SUPPORTED, f"op_{op}_f32")
+        _check(fn(self.handle, a.handle, b.handle, out.handle, n), f"op_{op}_f32")
+
+    def matmul_f32(self, a: Buffer, b: Buffer, out: Buffer, M: int, K: int, N: int) -> None:
+        _check(self.vt.op_matmul_f32(self.handle, a.handle, b.handle, out.handle, M, K, N), "op_matmul_f32")
+
+    def transpose_f32(self, a: Buffer, out: Buffer, rows: int, cols: int) -> None:
+        _check(self.vt.op_transpose_f32(self.handle, a.handle, out.handle, rows, cols), "op_transpose_f32")
+
 
 def esize(dtype: int) -> int:
     return _ESZ[dtype]
