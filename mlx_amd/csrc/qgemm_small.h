@@ -50,6 +50,14 @@ __device__ __forceinline__ void wait_vmcnt_small() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// wait until this wave's LDS reads have returned.  A ring slot is refilled
+// by a DMA one step after it was last read, and the compiler may leave one
+// of those reads in flight across the refill's issue: an LDS DMA write can
+// land before such a queued read executes (measured: stale operands in a
+// few blocks per launch, with all 256 CUs busy), so every refill waits for
+// the wave's outstanding reads first.
+__device__ __forceinline__ void wait_lds_reads() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 template <int SB>
 __device__ __forceinline__ float sb_val(uint32_t w) {
     if constexpr (SB == DT_F32) return __uint_as_float(w);
@@ -183,7 +191,9 @@ __device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, 
     using L = Lay<BITS, SB, MT, GS>;
     const int u = q >> 2;
     // issue: W/scales of super-step u + kRW - 1 (at P == 0), x of step q + kRX - 1
-    // (past the part's end they repeat its last super-step / step: counts stay fixed)
+    // (past the part's end they repeat its last super-step / step: counts stay
+    // fixed), once the previous step's reads of the refilled slots are done
+    wait_lds_reads();
     if constexpr (P == 0) {
         const int uw = u + L::kRW - 1, ul = (nq >> 2) - 1;
         issue_w(c, uw < ul ? uw : ul);

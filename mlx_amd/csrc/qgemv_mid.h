@@ -37,6 +37,7 @@ using small::dma16;
 using small::dma4;
 using small::swz;
 using small::wait_vmcnt_small;
+using small::wait_lds_reads;
 using skinny::Form;
 using skinny::code_operand;
 using skinny::x_operand;
@@ -123,6 +124,7 @@ __device__ __forceinline__ void step(f32x4 (&acc)[2], f32x4 (&dg)[2], f32x4& dx,
     using F = Form<BITS, TX>;
     constexpr int NMG = GS / 32;  // slices per group
     const int u = q >> 2;
+    wait_lds_reads();  // the previous step's reads of the slots refilled here are done
     if constexpr (P == 0) {
         const int uw = u + L::kRW - 1, ul = (nq >> 2) - 1;
         issue_w(c, uw < ul ? uw : ul);

@@ -301,6 +301,40 @@ def test_small_gemm_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"small gemm b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("M,K,N,bits,gs,xd,kern", [
+    (32, 8192, 8192, 8, 128, BF16, "gemm"),   # small-M GEMM, one block per CU
+    (64, 4096, 11008, 3, 64, F16, "gemm"),    # two M tiles, ragged grid
+    (16, 4096, 14336, 4, 64, BF16, "gemv"),   # mid-M GEMV rings
+])
+def test_ring_kernels_repeat_full_grid(ctx, oracle, M, K, N, bits, gs, xd, kern):
+    """The per-wave DMA ring kernels over a full grid (every CU busy), six
+    launches in a row: each equals the oracle and the first bit for bit.
+    A ring slot refilled while a read of its previous contents was still
+    queued once gave stale operands in a few blocks of such launches."""
+    O = oracle
+    from mlx_amd import abi
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, xd, seed=4000 + M)
+    gemm = kern == "gemm"
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, xd, F32, variant="omp",
+                              w_round=xd if gemm else F32)
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    out = ctx.alloc(M * N * 4)
+    try:
+        first = None
+        for rep in range(6):
+            print(f"[case] ring repeat {rep} M={M} K={K} N={N} b={bits} kernel={kern}", flush=True)
+            ctx.quantized_matmul(*bufs, out, M, K, N, gs, bits, xd, xd, F32,
+                                 abi.KERNEL_GEMM if gemm else abi.KERNEL_GEMV)
+            y = out.download(np.float32, (M, N))
+            check_output(O, y, want, F32, f"ring repeat {rep}")
+            if first is None:
+                first = y
+            assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), f"launch {rep} differs from launch 0"
+    finally:
+        for t in bufs + [out]:
+            t.free()
+
+
 def test_gemm_shape_limits(ctx, oracle):
     """K not a multiple of 256: an explicit GEMM request is NOT_SUPPORTED,
     AUTO picks the GEMV (exact weights) for any M."""
