@@ -46,6 +46,47 @@ typedef enum {
     LUX_QMM_KERNEL_GEMM = 2, /* MFMA GEMM (16-bit activations only) */
 } LuxQuantKernel;
 
+/* fused output stage of op_quantized_matmul_fused, applied in fp32 */
+typedef enum {
+    LUX_QMM_ACT_NONE = 0,
+    LUX_QMM_ACT_RELU = 1, /* v < 0 ? 0 : v (NaN passes through) */
+    LUX_QMM_ACT_SILU = 2, /* v / (1 + exp(-v)) */
+    LUX_QMM_ACT_GELU = 3, /* v/2 (1 + erf(v / sqrt(2))) */
+} LuxQuantAct;
+
+/*
+ * Quantized linear layers on disk (safetensors).  The file is a 64-bit
+ * little-endian header length H, H bytes of JSON, then the data; each JSON
+ * entry maps a tensor name to {"dtype", "shape", "data_offsets": [begin,
+ * end]} relative to the data.  A layer with name prefix P holds
+ *   P.weight  U32 [N, K*bits/32]      packed codes (the format above)
+ *   P.scales  F32|F16|BF16 [N, K/g]
+ *   P.biases  same dtype and shape as P.scales
+ *   P.bias    F32|F16|BF16 [N]        optional output bias (fused op)
+ * bits and group_size come from the caller, else from the "__metadata__"
+ * string entries "P.bits" / "P.group_size", else its "bits" / "group_size".
+ * No counterpart in the reference (it has no weight files).
+ */
+typedef struct lux_quant_linear_info {
+    int32_t N, K, group_size, bits;
+    LuxBackendDtype sb_dtype;   /* scales and biases */
+    LuxBackendDtype bias_dtype; /* P.bias, when has_bias */
+    int32_t has_bias;
+    int32_t _pad;
+    uint64_t weight_offset, weight_bytes; /* absolute file offsets of the data */
+    uint64_t scales_offset, scales_bytes;
+    uint64_t biases_offset, biases_bytes;
+    uint64_t bias_offset, bias_bytes;
+} lux_quant_linear_info;
+
+typedef struct lux_quant_linear {
+    lux_quant_linear_info info;
+    LuxBackendBuffer* w_q;
+    LuxBackendBuffer* scales;
+    LuxBackendBuffer* biases;
+    LuxBackendBuffer* bias; /* NULL without P.bias */
+} lux_quant_linear;
+
 typedef struct lux_gpu_quant_vtbl {
     uint32_t ext_version; /* LUX_GPU_QUANT_EXT_VERSION */
     uint32_t struct_size; /* sizeof(lux_gpu_quant_vtbl) of the plugin */
@@ -90,8 +131,55 @@ typedef struct lux_gpu_quant_vtbl {
     LuxQuantKernel (*select_kernel)(int M, int K, int N, int group_size, int bits,
                                     LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype);
 
-    void* _reserved[8];
+    /* out[m,n] = act(sum_k x[m,k] w_hat[n,k] + bias[n]): the bias (T_bias[N],
+     * or NULL for none) and the activation are applied in fp32 to the
+     * accumulator, before the one rounding to T_out, by the kernel that
+     * computes out (no second pass over out).  Same kernels, selection and
+     * errors as op_quantized_matmul; an unknown act is INVALID_ARGUMENT.
+     * No counterpart in the reference (it has no quantized or fused op);
+     * NULL in plugins that predate it. */
+    LuxBackendError (*op_quantized_matmul_fused)(LuxBackendContext* ctx, LuxBackendBuffer* x,
+                                                 LuxBackendBuffer* w_q, LuxBackendBuffer* scales,
+                                                 LuxBackendBuffer* biases, LuxBackendBuffer* bias,
+                                                 LuxBackendBuffer* out, int M, int K, int N,
+                                                 int group_size, int bits, LuxBackendDtype x_dtype,
+                                                 LuxBackendDtype sb_dtype, LuxBackendDtype bias_dtype,
+                                                 LuxBackendDtype out_dtype, LuxQuantAct act);
+
+    /* Parse the safetensors header of `path` and describe layer `prefix`
+     * (host only, no device work).  group_size / bits 0 = from the file.
+     * Unreadable or malformed file, missing tensor, shapes that disagree:
+     * INVALID_ARGUMENT; bits, group size or dtype outside the format:
+     * NOT_SUPPORTED. */
+    LuxBackendError (*linear_describe)(const char* path, const char* prefix, int group_size,
+                                       int bits, lux_quant_linear_info* out);
+
+    /* linear_describe, then one device buffer per tensor on ctx, filled from
+     * the memory-mapped file (synchronous: the data is on the device when it
+     * returns).  On error nothing stays allocated and *out is zeroed. */
+    LuxBackendError (*linear_load)(LuxBackendContext* ctx, const char* path, const char* prefix,
+                                   int group_size, int bits, lux_quant_linear* out);
+
+    /* frees the buffers linear_load allocated and zeroes *layer */
+    void (*linear_free)(LuxBackendContext* ctx, lux_quant_linear* layer);
+
+    void* _reserved[4];
 } lux_gpu_quant_vtbl;
+
+/* layout pins: LP64 */
+#if defined(__LP64__)
+#ifdef __cplusplus
+static_assert(sizeof(lux_gpu_quant_vtbl) == 120, "quant table size");
+static_assert(offsetof(lux_gpu_quant_vtbl, op_quantized_matmul_fused) == 56, "fused op slot");
+static_assert(offsetof(lux_gpu_quant_vtbl, linear_free) == 80, "weight file slots");
+static_assert(sizeof(lux_quant_linear_info) == 96, "linear info size");
+#else
+_Static_assert(sizeof(lux_gpu_quant_vtbl) == 120, "quant table size");
+_Static_assert(offsetof(lux_gpu_quant_vtbl, op_quantized_matmul_fused) == 56, "fused op slot");
+_Static_assert(offsetof(lux_gpu_quant_vtbl, linear_free) == 80, "weight file slots");
+_Static_assert(sizeof(lux_quant_linear_info) == 96, "linear info size");
+#endif
+#endif
 
 typedef bool (*lux_gpu_backend_quant_init_fn)(const lux_gpu_quant_vtbl** out);
 

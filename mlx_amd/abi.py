@@ -133,6 +133,29 @@ OP_DEQUANT = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, Buf, _I, _I, _I, _I, _I, _I)
 OP_QUANT = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, Buf, _I, _I, _I, _I, _I, _I)
 GET_NATIVE_STREAM = C.CFUNCTYPE(C.c_void_p, Ctx)
 SELECT_KERNEL = C.CFUNCTYPE(_I, _I, _I, _I, _I, _I, _I, _I)
+# ctx, x, w_q, scales, biases, bias, out, M, K, N, group_size, bits, x_dt, sb_dt, bias_dt, out_dt, act
+OP_QMM_FUSED = C.CFUNCTYPE(Err, Ctx, Buf, Buf, Buf, Buf, Buf, Buf, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I)
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU = 0, 1, 2, 3
+
+
+class LinearInfo(C.Structure):
+    """lux_quant_linear_info: a quantized linear layer in a safetensors file."""
+    _fields_ = [("N", C.c_int32), ("K", C.c_int32), ("group_size", C.c_int32), ("bits", C.c_int32),
+                ("sb_dtype", C.c_int), ("bias_dtype", C.c_int), ("has_bias", C.c_int32), ("_pad", C.c_int32),
+                ("weight_offset", C.c_uint64), ("weight_bytes", C.c_uint64),
+                ("scales_offset", C.c_uint64), ("scales_bytes", C.c_uint64),
+                ("biases_offset", C.c_uint64), ("biases_bytes", C.c_uint64),
+                ("bias_offset", C.c_uint64), ("bias_bytes", C.c_uint64)]
+
+
+class Linear(C.Structure):
+    """lux_quant_linear: the layer's device buffers after linear_load."""
+    _fields_ = [("info", LinearInfo), ("w_q", Buf), ("scales", Buf), ("biases", Buf), ("bias", Buf)]
+
+
+LINEAR_DESCRIBE = C.CFUNCTYPE(Err, C.c_char_p, C.c_char_p, _I, _I, C.POINTER(LinearInfo))
+LINEAR_LOAD = C.CFUNCTYPE(Err, Ctx, C.c_char_p, C.c_char_p, _I, _I, C.POINTER(Linear))
+LINEAR_FREE = C.CFUNCTYPE(None, Ctx, C.POINTER(Linear))
 
 
 class QuantVtbl(C.Structure):
@@ -145,7 +168,11 @@ class QuantVtbl(C.Structure):
         ("op_quantized_matmul_ex", OP_QMM_EX),
         ("get_native_stream", GET_NATIVE_STREAM),
         ("select_kernel", SELECT_KERNEL),
-        ("_reserved", C.c_void_p * 8),
+        ("op_quantized_matmul_fused", OP_QMM_FUSED),
+        ("linear_describe", LINEAR_DESCRIBE),
+        ("linear_load", LINEAR_LOAD),
+        ("linear_free", LINEAR_FREE),
+        ("_reserved", C.c_void_p * 4),
     ]
 
 
@@ -161,6 +188,8 @@ def check_layout() -> None:
     assert BackendVtbl._reserved.offset == 480
     assert C.sizeof(BackendDesc) == 40 and BackendDesc.vtbl.offset == 32
     assert C.sizeof(DeviceInfo) == 48 and DeviceInfo.is_unified_memory.offset == 41
+    assert C.sizeof(QuantVtbl) == 8 + 14 * 8 and QuantVtbl.op_quantized_matmul_fused.offset == 8 + 6 * 8
+    assert QuantVtbl.linear_free.offset == 80 and C.sizeof(LinearInfo) == 96
 
 
 check_layout()

@@ -1,6 +1,7 @@
 """Build libluxgpu_backend_hip.so in-tree with hipcc for gfx950.
 
-The plugin is compiled from mlx_amd/csrc/*.hip into mlx_amd/lib/.  Every
+The plugin is compiled from mlx_amd/csrc/*.hip (hipcc, gfx950) and the
+host-only mlx_amd/csrc/*.cpp (g++) into mlx_amd/lib/.  Every
 source is compiled each time build() runs (the driver's "does it build"
 check); objects land in mlx_amd/_build/ and are linked into one shared
 library whose only exported symbols are the two plugin entry points.
@@ -33,19 +34,30 @@ CFLAGS = [
 ]
 
 
+CXX = os.environ.get("CXX", "g++")
+CXXFLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra"]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [CXX, *CXXFLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
+        raise RuntimeError(f"compile failed on {src}:\n{r.stdout}\n{r.stderr}")
     return obj
+
+
+def sources() -> list:
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
 
 
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = PLUGIN + ".tmp"

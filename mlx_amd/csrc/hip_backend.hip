@@ -23,6 +23,7 @@
 #include "../../include/lux_gpu_backend_abi.h"
 #include "../../include/lux_gpu_quant_backend.h"
 #include "kernels.h"
+#include "qweights.h"
 
 namespace {
 
@@ -293,13 +294,16 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
                          LuxBackendBuffer* scales, LuxBackendBuffer* biases,
                          LuxBackendBuffer* out, int M, int K, int N, int group_size, int bits,
                          LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype,
-                         LuxBackendDtype out_dtype, LuxQuantKernel kernel) {
+                         LuxBackendDtype out_dtype, LuxQuantKernel kernel,
+                         LuxBackendBuffer* bias = nullptr, LuxBackendDtype bias_dtype = LUX_DTYPE_FLOAT32,
+                         int act = LUX_QMM_ACT_NONE) {
     HipContext* ctx = C(c);
     if (!ctx || !x || !w_q || !scales || !biases || !out) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (act < LUX_QMM_ACT_NONE || act > LUX_QMM_ACT_GELU) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
     if (M < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
     LuxBackendError e = check_format(K, N, group_size, bits);
     if (e != LUX_BACKEND_OK) return e;
-    if (!dtype_ok(x_dtype) || !dtype_ok(sb_dtype) || !dtype_ok(out_dtype))
+    if (!dtype_ok(x_dtype) || !dtype_ok(sb_dtype) || !dtype_ok(out_dtype) || (bias && !dtype_ok(bias_dtype)))
         return LUX_BACKEND_ERROR_NOT_SUPPORTED;
     if (kernel != LUX_QMM_KERNEL_AUTO && kernel != LUX_QMM_KERNEL_GEMV && kernel != LUX_QMM_KERNEL_GEMM)
         return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
@@ -307,7 +311,8 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     if (!fits(B(x), (size_t)M * K * dtype_size(x_dtype)) ||
         !fits(B(w_q), (size_t)N * K * bits / 8) || !fits(B(scales), (size_t)N * G * dtype_size(sb_dtype)) ||
         !fits(B(biases), (size_t)N * G * dtype_size(sb_dtype)) ||
-        !fits(B(out), (size_t)M * N * dtype_size(out_dtype)))
+        !fits(B(out), (size_t)M * N * dtype_size(out_dtype)) ||
+        (bias && !fits(B(bias), (size_t)N * dtype_size(bias_dtype))))
         return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
     if (M == 0 || N == 0) return LUX_BACKEND_OK;
 
@@ -319,6 +324,9 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     a.y = B(out)->ptr;
     a.M = M; a.K = K; a.N = N; a.group_size = group_size; a.bits = bits;
     a.x_dtype = x_dtype; a.sb_dtype = sb_dtype; a.out_dtype = out_dtype;
+    a.bias = bias ? B(bias)->ptr : nullptr;
+    a.bias_dtype = bias_dtype;
+    a.act = act;
 
     if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
     if (kernel == LUX_QMM_KERNEL_AUTO)
@@ -354,6 +362,17 @@ LuxBackendError hip_op_quantized_matmul_ex(LuxBackendContext* c, LuxBackendBuffe
                                            LuxBackendDtype out_dtype, LuxQuantKernel kernel) {
     return qmm_impl(c, x, w_q, scales, biases, out, M, K, N, group_size, bits, x_dtype, sb_dtype,
                     out_dtype, kernel);
+}
+
+LuxBackendError hip_op_quantized_matmul_fused(LuxBackendContext* c, LuxBackendBuffer* x,
+                                              LuxBackendBuffer* w_q, LuxBackendBuffer* scales,
+                                              LuxBackendBuffer* biases, LuxBackendBuffer* bias,
+                                              LuxBackendBuffer* out, int M, int K, int N,
+                                              int group_size, int bits, LuxBackendDtype x_dtype,
+                                              LuxBackendDtype sb_dtype, LuxBackendDtype bias_dtype,
+                                              LuxBackendDtype out_dtype, LuxQuantAct act) {
+    return qmm_impl(c, x, w_q, scales, biases, out, M, K, N, group_size, bits, x_dtype, sb_dtype,
+                    out_dtype, LUX_QMM_KERNEL_AUTO, bias, bias_dtype, (int)act);
 }
 
 LuxBackendError hip_op_dequantize(LuxBackendContext* c, LuxBackendBuffer* w_q,
@@ -464,6 +483,48 @@ LuxQuantKernel hip_select_kernel(int M, int K, int N, int group_size, int bits,
     return select_kernel_impl(M, K, N, group_size, bits, x_dtype, sb_dtype);
 }
 
+// ---- quantized linear layers from safetensors files ----------------------
+
+LuxBackendError hip_linear_describe(const char* path, const char* prefix, int group_size, int bits,
+                                    lux_quant_linear_info* out) {
+    return lxq::linear_describe(path, prefix, group_size, bits, out);
+}
+
+void hip_linear_free(LuxBackendContext* c, lux_quant_linear* l) {
+    if (!l) return;
+    for (LuxBackendBuffer* b : {l->w_q, l->scales, l->biases, l->bias})
+        if (b) hip_buffer_free(c, b);
+    std::memset(l, 0, sizeof(*l));
+}
+
+LuxBackendError hip_linear_load(LuxBackendContext* c, const char* path, const char* prefix, int group_size,
+                                int bits, lux_quant_linear* out) {
+    if (!out) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    std::memset(out, 0, sizeof(*out));
+    if (!C(c)) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    lux_quant_linear_info info;
+    LuxBackendError e = lxq::linear_describe(path, prefix, group_size, bits, &info);
+    if (e != LUX_BACKEND_OK) return e;
+    lxq::MappedFile f;
+    if (!f.open(path)) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    // the file may have changed since it was described: re-check the ranges
+    const uint64_t ranges[4][2] = {{info.weight_offset, info.weight_bytes}, {info.scales_offset, info.scales_bytes},
+                                   {info.biases_offset, info.biases_bytes}, {info.bias_offset, info.bias_bytes}};
+    for (const auto& r : ranges)
+        if (r[0] > f.size || r[1] > f.size - r[0]) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    LuxBackendBuffer** dst[4] = {&out->w_q, &out->scales, &out->biases, &out->bias};
+    for (int i = 0; i < 4; i++) {
+        if (i == 3 && !info.has_bias) break;
+        *dst[i] = hip_buffer_alloc_with_data(c, f.data + ranges[i][0], ranges[i][1]);
+        if (!*dst[i]) {
+            hip_linear_free(c, out);
+            return LUX_BACKEND_ERROR_OUT_OF_MEMORY;
+        }
+    }
+    out->info = info;
+    return LUX_BACKEND_OK;
+}
+
 // ---------------------------------------------------------------------------
 // tables
 // ---------------------------------------------------------------------------
@@ -504,6 +565,10 @@ lux_gpu_quant_vtbl make_qvtbl() {
     q.op_quantized_matmul_ex = hip_op_quantized_matmul_ex;
     q.get_native_stream = hip_get_native_stream;
     q.select_kernel = hip_select_kernel;
+    q.op_quantized_matmul_fused = hip_op_quantized_matmul_fused;
+    q.linear_describe = hip_linear_describe;
+    q.linear_load = hip_linear_load;
+    q.linear_free = hip_linear_free;
     return q;
 }
 

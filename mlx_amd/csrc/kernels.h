@@ -16,6 +16,17 @@ enum class LuxStatus : int { Ok = 0, Invalid = 1, OutOfMemory = 2, NotSupported 
 // 16-byte chunks.
 constexpr size_t kTailPad = 256;
 
+// Output stage shared by the matmul kernels: y[m, n] = act(acc + bias[n])
+// in fp32, then rounded (RNE) to out_dt.  relu(v) = v < 0 ? 0 : v (NaN
+// passes), silu(v) = v / (1 + exp(-v)), gelu(v) = v/2 (1 + erf(v / sqrt 2)).
+enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SILU = 2, ACT_GELU = 3 };
+struct Epilogue {
+    const void* bias;  // [N] in bias_dt, or nullptr
+    int bias_dt;
+    int act;
+    int out_dt;
+};
+
 struct QmmArgs {
     const void* x;        // [M, K] x_dtype
     const uint32_t* wq;   // [N, K*bits/32]
@@ -24,6 +35,13 @@ struct QmmArgs {
     void* y;              // [M, N] out_dtype
     int M, K, N, group_size, bits;
     int x_dtype, sb_dtype, out_dtype;
+    const void* bias = nullptr;  // fused epilogue: per-column bias [N] (bias_dtype) or none
+    int bias_dtype = 0;
+    int act = ACT_NONE;
+    Epilogue epi() const { return Epilogue{bias, bias_dtype, act, out_dtype}; }
+    // kernels are instantiated with and without the output stage: the plain
+    // op runs code with no bias or activation path at all
+    bool has_epilogue() const { return bias != nullptr || act != ACT_NONE; }
 };
 
 // bandwidth-bound dequant-GEMV (any M; tuned for M <= 8); needs K % 64 == 0

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kernels.h"
+
 namespace lxq {
 
 enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
@@ -45,6 +47,22 @@ __device__ __forceinline__ void store_f(void* p, size_t i, int dt, float v) {
     if (dt == DT_F32) reinterpret_cast<float*>(p)[i] = v;
     else if (dt == DT_F16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16(v);
     else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// the output stage (Epilogue, kernels.h) for column n, then the store
+__device__ __forceinline__ float apply_epilogue(const Epilogue& e, size_t n, float v) {
+    if (e.bias) v = v + load_f(e.bias, n, e.bias_dt);
+    if (e.act == ACT_RELU) v = v < 0.f ? 0.f : v;
+    else if (e.act == ACT_SILU) v = v / (1.f + expf(-v));
+    else if (e.act == ACT_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    return v;
+}
+// EPI: the kernel instantiation that applies the output stage (else only
+// the store; out_dt is read from e in both)
+template <bool EPI>
+__device__ __forceinline__ void store_out(void* y, size_t i, size_t n, const Epilogue& e, float v) {
+    if constexpr (EPI) v = apply_epilogue(e, n, v);
+    store_f(y, i, e.out_dt, v);
 }
 
 // code i (0..63) of a 64-code unit held in 2*BITS words w[] (compile-time i

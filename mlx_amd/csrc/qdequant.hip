@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void qmm_generic_kernel(const void* __restrict
                                                           const void* __restrict__ bi,
                                                           void* __restrict__ y, int M, int K,
                                                           int N, int gsize, int bits, int x_dt,
-                                                          int sb_dt, int out_dt) {
+                                                          int sb_dt, Epilogue ep) {
 #pragma clang fp contract(off)
     const size_t total = (size_t)M * N;
     const int G = K / gsize, rw = (K * bits) >> 5;
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void qmm_generic_kernel(const void* __restrict
                                   load_f(bi, gi, sb_dt));
             acc = acc + load_f(x, (size_t)m * K + k, x_dt) * wv;
         }
-        store_f(y, i, out_dt, acc);
+        store_out<true>(y, i, n, ep, acc);
     }
 }
 
@@ -212,7 +212,7 @@ LuxStatus launch_qmm_generic(const QmmArgs& a, hipStream_t st) {
     if (total == 0) return LuxStatus::Ok;
     hipLaunchKernelGGL(qmm_generic_kernel, dim3(grid_for(total)), dim3(256), 0, st, a.x, a.wq,
                        a.scales, a.biases, a.y, a.M, a.K, a.N, a.group_size, a.bits, a.x_dtype,
-                       a.sb_dtype, a.out_dtype);
+                       a.sb_dtype, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 

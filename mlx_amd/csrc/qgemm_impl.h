@@ -490,10 +490,10 @@ __device__ __forceinline__ void main_loop(f32x16 (&acc)[2][2], const Ctx& t, con
     wait_vmcnt<0>();
 }
 
-template <int TX, int BITS, int SB, int GS>
+template <int TX, int BITS, int SB, int GS, bool EPI>
 __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int out_dt,
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep,
     int mtiles) {
     static_assert(lds_fits<BITS, GS, SB>(), "LDS budget");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -549,9 +549,9 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     // VGPR v holds row 8 (v / 4) + 4 (lane / 32) + v % 4 ----
     const int ncol = t.n0 + wn * 64 + (lane & 31);
     const int mrow = m0 + wm * 64 + 4 * (lane >> 5);
-    if (out_dt == DT_BF16 || out_dt == DT_F16) {
+    if (ep.out_dt == DT_BF16 || ep.out_dt == DT_F16) {
         uint16_t* yo = static_cast<uint16_t*>(y);
-        const bool bf = out_dt == DT_BF16;
+        const bool bf = ep.out_dt == DT_BF16;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -560,8 +560,10 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                     const int m = mrow + i * 32 + 8 * (v >> 2) + (v & 3);
-                    if (m < M && n < N)
-                        yo[(size_t)m * N + n] = bf ? f32_to_bf16(acc[i][j][v]) : f32_to_f16(acc[i][j][v]);
+                    if (m < M && n < N) {
+                        const float o = EPI ? apply_epilogue(ep, n, acc[i][j][v]) : acc[i][j][v];
+                        yo[(size_t)m * N + n] = bf ? f32_to_bf16(o) : f32_to_f16(o);
+                    }
                 }
             }
     } else {
@@ -574,18 +576,18 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                     const int m = mrow + i * 32 + 8 * (v >> 2) + (v & 3);
-                    if (m < M && n < N) yo[(size_t)m * N + n] = acc[i][j][v];
+                    if (m < M && n < N) yo[(size_t)m * N + n] = EPI ? apply_epilogue(ep, n, acc[i][j][v]) : acc[i][j][v];
                 }
             }
     }
 }
 
-template <int TX, int BITS, int SB, int GS>
-LuxStatus launch4(const QmmArgs& a, hipStream_t st) {
+template <int TX, int BITS, int SB, int GS, bool EPI>
+LuxStatus launch4_e(const QmmArgs& a, hipStream_t st) {
     if constexpr (!lds_fits<BITS, GS, SB>()) {
         return LuxStatus::NotSupported;
     } else {
-        auto kern = qgemm_kernel<TX, BITS, SB, GS>;
+        auto kern = qgemm_kernel<TX, BITS, SB, GS, EPI>;
         constexpr size_t lds = lds_bytes<BITS, GS, SB>();
         static const hipError_t attr = hipFuncSetAttribute(
             reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -593,9 +595,14 @@ LuxStatus launch4(const QmmArgs& a, hipStream_t st) {
         const int mtiles = (a.M + BM - 1) / BM, ntiles = (a.N + BN - 1) / BN;
         hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(kThreads), lds, st,
                            static_cast<const uint16_t*>(a.x), a.wq, a.scales, a.biases, a.y, a.M, a.K,
-                           a.N, a.out_dtype, mtiles);
+                           a.N, a.epi(), mtiles);
         return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
     }
+}
+
+template <int TX, int BITS, int SB, int GS>
+LuxStatus launch4(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch4_e<TX, BITS, SB, GS, true>(a, st) : launch4_e<TX, BITS, SB, GS, false>(a, st);
 }
 
 template <int TX, int BITS, int GS>

@@ -238,10 +238,10 @@ __device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, 
     }
 }
 
-template <int BITS, int TX, int SB, int MT, int GS>
+template <int BITS, int TX, int SB, int MT, int GS, bool EPI>
 __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int out_dt) {
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep) {
     using L = Lay<BITS, SB, MT, GS>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
             for (int w2 = 0; w2 < kWaves; w2++) sum += red[((size_t)w2 * MT * 16 + t * 16 + v) * 64 + lane];
             // 32x32 accumulator layout: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
             const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (m < M && nn < N) store_f(y, (size_t)m * N + nn, out_dt, sum);
+            if (m < M && nn < N) store_out<EPI>(y, (size_t)m * N + nn, nn, ep, sum);
         }
 }
 

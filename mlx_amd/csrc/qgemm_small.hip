@@ -4,11 +4,11 @@
 namespace lxq {
 namespace small {
 
-template <int BITS, int TX, int SB, int MT, int GS>
-LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+template <int BITS, int TX, int SB, int MT, int GS, bool EPI>
+LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     using L = Lay<BITS, SB, MT, GS>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
-    auto kern = qgemm_small_kernel<BITS, TX, SB, MT, GS>;
+    auto kern = qgemm_small_kernel<BITS, TX, SB, MT, GS, EPI>;
     static bool attr_set = false;  // one per instantiation
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -17,8 +17,14 @@ LuxStatus launch(const QmmArgs& a, hipStream_t st) {
         attr_set = true;
     }
     hipLaunchKernelGGL(kern, dim3((a.N + 31) / 32), dim3(64 * kWaves), L::kBytes, st, a.x, a.wq, a.scales, a.biases,
-                       a.y, a.M, a.K, a.N, a.out_dtype);
+                       a.y, a.M, a.K, a.N, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int BITS, int TX, int SB, int MT, int GS>
+LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch_e<BITS, TX, SB, MT, GS, true>(a, st)
+                            : launch_e<BITS, TX, SB, MT, GS, false>(a, st);
 }
 
 template <int BITS, int TX, int SB, int MT>

@@ -131,11 +131,11 @@ __host__ __device__ constexpr size_t dec_lds_bytes(int M, int K) {
     return (size_t)M * (2 * K + 16) + (size_t)(K / kKW - 1) * kTiles * 4 * 64 * 4;
 }
 
-template <int TX, int SB, int GS>
+template <int TX, int SB, int GS, bool EPI>
 __global__ __launch_bounds__(512) void qgemv_dec_kernel(const void* __restrict__ x, const uint32_t* __restrict__ wq,
                                                         const void* __restrict__ scales,
                                                         const void* __restrict__ biases, void* __restrict__ y,
-                                                        int M, int K, int N, int out_dt) {
+                                                        int M, int K, int N, Epilogue ep) {
     using F = DForm<TX>;
     using Q = DGeo<GS, SB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(512) void qgemv_dec_kernel(const void* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = 4 * c + r;
-                if (m < M && n < N) store_f(y, (size_t)m * N + n, out_dt, acc[t][r] * F::kPow);
+                if (m < M && n < N) store_out<EPI>(y, (size_t)m * N + n, n, ep, acc[t][r] * F::kPow);
             }
         }
     }

@@ -4,11 +4,11 @@
 namespace lxq {
 namespace dec {
 
-template <int TX, int SB, int GS>
-LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+template <int TX, int SB, int GS, bool EPI>
+LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     const size_t lds = dec_lds_bytes(a.M, a.K);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
-    auto kern = qgemv_dec_kernel<TX, SB, GS>;
+    auto kern = qgemv_dec_kernel<TX, SB, GS, EPI>;
     static bool attr_set = false;  // one per instantiation
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -18,8 +18,13 @@ LuxStatus launch(const QmmArgs& a, hipStream_t st) {
     }
     const int blocks = (a.N + 16 * kTiles - 1) / (16 * kTiles);
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * (a.K / kKW)), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.M,
-                       a.K, a.N, a.out_dtype);
+                       a.K, a.N, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int TX, int SB, int GS>
+LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch_e<TX, SB, GS, true>(a, st) : launch_e<TX, SB, GS, false>(a, st);
 }
 
 template <int TX, int SB>

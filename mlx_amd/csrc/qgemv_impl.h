@@ -47,11 +47,11 @@ __device__ __forceinline__ void load_unit(const uint32_t* __restrict__ p, uint32
     }
 }
 
-template <int BITS, int TX, int MR, int RU>
+template <int BITS, int TX, int MR, int RU, bool EPI>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int gsize,
-    int sb_dt, int out_dt, int rows_per_wave) {
+    int sb_dt, Epilogue ep, int rows_per_wave) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     using XL = XLds<TX>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
 #pragma unroll
             for (int m = 0; m < MR; m++) {
                 const float v = wave_sum(acc[r][m]);
-                if (lane == 0 && m < M && n0 + r < n_end) store_f(y, (size_t)m * N + n0 + r, out_dt, v);
+                if (lane == 0 && m < M && n0 + r < n_end) store_out<EPI>(y, (size_t)m * N + n0 + r, n0 + r, ep, v);
             }
         }
     }
@@ -480,11 +480,11 @@ __device__ __host__ __forceinline__ int sum8_index(int lane) {
     return 4 * half + (((row & 1) << 1) | (row >> 1));
 }
 
-template <int BITS, int TX, int SB, int MR, int R, bool TWO>
+template <int BITS, int TX, int SB, int MR, int R, bool TWO, bool EPI>
 __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int gshift,
-    int out_dt) {
+    Epilogue ep) {
     using L = StreamLds<TX, SB, MR, R>;
     constexpr int OP = op_kind<BITS, TX>();
     constexpr int XE = TX == DT_F32 ? 4 : 2;
@@ -604,24 +604,30 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
         const float z = sum8(acc + 8 * c, lane) * out_scale<OP>();
         const int v = 8 * c + sum8_index(lane);
         const int r = v / MR, m = v % MR;
-        if ((lane & 7) == 0 && v < V && m < M && n0 + r < N) store_f(y, (size_t)m * N + n0 + r, out_dt, z);
+        if ((lane & 7) == 0 && v < V && m < M && n0 + r < N) store_out<EPI>(y, (size_t)m * N + n0 + r, n0 + r, ep, z);
     }
 }
 
-template <int BITS, int TX, int SB, int MR, int R>
-LuxStatus launch_stream(const QmmArgs& a, hipStream_t st) {
+template <int BITS, int TX, int SB, int MR, int R, bool EPI>
+LuxStatus launch_stream_e(const QmmArgs& a, hipStream_t st) {
     const int rows = kStreamWaves * R;
     const int blocks = (a.N + rows - 1) / rows;
     const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
     if (a.group_size == 32)
-        hipLaunchKernelGGL((qgemv_stream_kernel<BITS, TX, SB, MR, R, true>), dim3(blocks),
+        hipLaunchKernelGGL((qgemv_stream_kernel<BITS, TX, SB, MR, R, true, EPI>), dim3(blocks),
                            dim3(64 * kStreamWaves), 0, st, a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K,
-                           a.N, gshift, a.out_dtype);
+                           a.N, gshift, a.epi());
     else
-        hipLaunchKernelGGL((qgemv_stream_kernel<BITS, TX, SB, MR, R, false>), dim3(blocks),
+        hipLaunchKernelGGL((qgemv_stream_kernel<BITS, TX, SB, MR, R, false, EPI>), dim3(blocks),
                            dim3(64 * kStreamWaves), 0, st, a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K,
-                           a.N, gshift, a.out_dtype);
+                           a.N, gshift, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int BITS, int TX, int SB, int MR, int R>
+LuxStatus launch_stream(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch_stream_e<BITS, TX, SB, MR, R, true>(a, st)
+                            : launch_stream_e<BITS, TX, SB, MR, R, false>(a, st);
 }
 
 // rows per wave: 4 (measured over R = 2..7 at K = 4096: equal to R = 7 at
@@ -637,8 +643,8 @@ LuxStatus launch_stream_r(const QmmArgs& a, hipStream_t st) {
     }
 }
 
-template <int BITS, int TX, int MR>
-LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
+template <int BITS, int TX, int MR, bool EPI>
+LuxStatus launch_t_e(const QmmArgs& a, hipStream_t st) {
     constexpr int RU = 4;
     using XL = XLds<TX>;
     const int units = a.K / 64;
@@ -652,7 +658,7 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
     if (rpw < RU) rpw = RU;
     const int waves = (a.N + rpw - 1) / rpw;
     const int blocks = (waves + 3) / 4;
-    auto kern = qgemv_kernel<BITS, TX, MR, RU>;
+    auto kern = qgemv_kernel<BITS, TX, MR, RU, EPI>;
     static bool attr_set = false;
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -661,8 +667,13 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
         attr_set = true;
     }
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a.x, a.wq, a.scales, a.biases,
-                       a.y, a.M, a.K, a.N, a.group_size, a.sb_dtype, a.out_dtype, rpw);
+                       a.y, a.M, a.K, a.N, a.group_size, a.sb_dtype, a.epi(), rpw);
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int BITS, int TX, int MR>
+LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch_t_e<BITS, TX, MR, true>(a, st) : launch_t_e<BITS, TX, MR, false>(a, st);
 }
 
 template <int BITS, int TX>

@@ -183,10 +183,10 @@ __device__ __forceinline__ void step(f32x4 (&acc)[2], f32x4 (&dg)[2], f32x4& dx,
     }
 }
 
-template <int BITS, int TX, int SB, int GS, int XR>
+template <int BITS, int TX, int SB, int GS, int XR, bool EPI>
 __global__ __launch_bounds__(64 * kWaves) void qgemv_mid_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int out_dt) {
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep) {
     using L = Lay<BITS, SB, GS, XR>;
     using F = Form<BITS, TX>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(64 * kWaves) void qgemv_mid_kernel(
         for (int w2 = 0; w2 < kWaves; w2++) sum += red[((w2 * 2 + t) * 4 + wave) * 64 + lane];
         // 16x16 accumulator: lane holds D[4 (lane / 16) + e][lane % 16] (rows m of x, columns n of W)
         const int mm = 4 * cg + wave, nn = n0 + 16 * t + j;
-        if (mm < M && nn < N) store_f(y, (size_t)mm * N + nn, out_dt, sum * F::kPow);
+        if (mm < M && nn < N) store_out<EPI>(y, (size_t)mm * N + nn, nn, ep, sum * F::kPow);
     }
 }
 

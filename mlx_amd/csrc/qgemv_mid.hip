@@ -4,11 +4,11 @@
 namespace lxq {
 namespace mid {
 
-template <int BITS, int TX, int SB, int GS, int XR>
-LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+template <int BITS, int TX, int SB, int GS, int XR, bool EPI>
+LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     using L = Lay<BITS, SB, GS, XR>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
-    auto kern = qgemv_mid_kernel<BITS, TX, SB, GS, XR>;
+    auto kern = qgemv_mid_kernel<BITS, TX, SB, GS, XR, EPI>;
     static bool attr_set = false;  // one per instantiation
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -17,8 +17,14 @@ LuxStatus launch(const QmmArgs& a, hipStream_t st) {
         attr_set = true;
     }
     hipLaunchKernelGGL(kern, dim3((a.N + 31) / 32), dim3(64 * kWaves), L::kBytes, st, a.x, a.wq, a.scales, a.biases,
-                       a.y, a.M, a.K, a.N, a.out_dtype);
+                       a.y, a.M, a.K, a.N, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int BITS, int TX, int SB, int GS, int XR>
+LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch_e<BITS, TX, SB, GS, XR, true>(a, st)
+                            : launch_e<BITS, TX, SB, GS, XR, false>(a, st);
 }
 
 // one x DMA (8 rows) per step for M <= 8, two for M <= 16

@@ -143,10 +143,10 @@ __host__ __device__ constexpr size_t skinny_lds_bytes(int M, int K, int G, int s
     return (size_t)M * (2 * K + 16) + 2 * (size_t)16 * tiles * G * sb_size + (size_t)(kWaves - tiles) * 64 * 16;
 }
 
-template <int BITS, int TX, int SB, int GS, int GW>
+template <int BITS, int TX, int SB, int GS, int GW, bool EPI>
 __global__ __launch_bounds__(64 * kWaves) void qmm_skinny_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int KS, int out_dt) {
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int KS, Epilogue ep) {
     using F = Form<BITS, TX>;
     using Q = Geo<BITS, GS>;
     constexpr int kSb = SB == DT_F32 ? 4 : 2;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(64 * kWaves) void qmm_skinny_kernel(
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int n = n_tile + 4 * c + r;
-            if (n < N) store_f(y, (size_t)j * N + n, out_dt, acc[r] * F::kPow);
+            if (n < N) store_out<EPI>(y, (size_t)j * N + n, n, ep, acc[r] * F::kPow);
         }
     }
 }

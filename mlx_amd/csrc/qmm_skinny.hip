@@ -4,13 +4,13 @@
 namespace lxq {
 namespace skinny {
 
-template <int BITS, int TX, int SB, int GS, int GW>
-LuxStatus launch(const QmmArgs& a, int KS, hipStream_t st) {
+template <int BITS, int TX, int SB, int GS, int GW, bool EPI>
+LuxStatus launch_e(const QmmArgs& a, int KS, hipStream_t st) {
     constexpr int kSb = SB == DT_F32 ? 4 : 2;
     const int tiles = kWaves / KS;
     const size_t lds = skinny_lds_bytes(a.M, a.K, a.K / GS, kSb, tiles);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
-    auto kern = qmm_skinny_kernel<BITS, TX, SB, GS, GW>;
+    auto kern = qmm_skinny_kernel<BITS, TX, SB, GS, GW, EPI>;
     static bool attr_set = false;  // one per instantiation
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -21,8 +21,14 @@ LuxStatus launch(const QmmArgs& a, int KS, hipStream_t st) {
     const int rows = 16 * tiles;
     const int blocks = (a.N + rows - 1) / rows;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * kWaves), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.M,
-                       a.K, a.N, KS, a.out_dtype);
+                       a.K, a.N, KS, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int BITS, int TX, int SB, int GS, int GW>
+LuxStatus launch(const QmmArgs& a, int KS, hipStream_t st) {
+    return a.has_epilogue() ? launch_e<BITS, TX, SB, GS, GW, true>(a, KS, st)
+                            : launch_e<BITS, TX, SB, GS, GW, false>(a, KS, st);
 }
 
 // groups per wave GW in {8, 16, 32}; the 8-bit, group-128 slice of 8 words

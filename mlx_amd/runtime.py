@@ -128,6 +128,25 @@ class Context:
                                              x_dtype, sb_dtype, out_dtype, kernel),
                "op_quantized_matmul")
 
+    def quantized_matmul_fused(self, x: Buffer, w_q: Buffer, scales: Buffer, biases: Buffer,
+                               bias: Optional[Buffer], out: Buffer, M: int, K: int, N: int,
+                               group_size: int, bits: int, x_dtype: int, sb_dtype: int,
+                               bias_dtype: int, out_dtype: int, act: int = abi.ACT_NONE) -> None:
+        """out = act(x . w_hat^T + bias), bias/act applied in fp32 in the kernel."""
+        _check(self.q.op_quantized_matmul_fused(self.handle, x.handle, w_q.handle, scales.handle,
+                                                biases.handle, bias.handle if bias else None,
+                                                out.handle, M, K, N, group_size, bits, x_dtype,
+                                                sb_dtype, bias_dtype, out_dtype, act),
+               "op_quantized_matmul_fused")
+
+    def load_linear(self, path: str, prefix: str, group_size: int = 0, bits: int = 0) -> "LinearLayer":
+        """A quantized linear layer from a safetensors file, on this context's
+        device (group_size / bits 0: from the file's metadata)."""
+        lin = abi.Linear()
+        _check(self.q.linear_load(self.handle, path.encode(), prefix.encode(), group_size, bits,
+                                  ctypes.byref(lin)), "linear_load")
+        return LinearLayer(self, lin)
+
     def dequantize(self, w_q: Buffer, scales: Buffer, biases: Buffer, out: Buffer, N: int, K: int,
                    group_size: int, bits: int, sb_dtype: int, out_dtype: int) -> None:
         _check(self.q.op_dequantize(self.handle, w_q.handle, scales.handle, biases.handle,
@@ -156,6 +175,45 @@ class Context:
 
     def transpose_f32(self, a: Buffer, out: Buffer, rows: int, cols: int) -> None:
         _check(self.vt.op_transpose_f32(self.handle, a.handle, out.handle, rows, cols), "op_transpose_f32")
+
+
+class LinearLayer:
+    """Device buffers of one quantized linear layer (lux_quant_linear)."""
+
+    def __init__(self, ctx: Context, lin: "abi.Linear"):
+        self.ctx, self.lin = ctx, lin
+        i = lin.info
+        self.N, self.K, self.group_size, self.bits = i.N, i.K, i.group_size, i.bits
+        self.sb_dtype, self.bias_dtype, self.has_bias = i.sb_dtype, i.bias_dtype, bool(i.has_bias)
+        self.w_q = Buffer(ctx, lin.w_q, i.weight_bytes)
+        self.scales = Buffer(ctx, lin.scales, i.scales_bytes)
+        self.biases = Buffer(ctx, lin.biases, i.biases_bytes)
+        self.bias = Buffer(ctx, lin.bias, i.bias_bytes) if lin.bias else None
+
+    def __call__(self, x: Buffer, out: Buffer, M: int, x_dtype: int, out_dtype: int,
+                 act: int = abi.ACT_NONE, use_bias: bool = True) -> None:
+        """out[M, N] = act(x . W^T + bias): the fused op, with the file's bias if it has one."""
+        bias = self.bias if (use_bias and self.has_bias) else None
+        self.ctx.quantized_matmul_fused(x, self.w_q, self.scales, self.biases, bias, out, M, self.K,
+                                        self.N, self.group_size, self.bits, x_dtype, self.sb_dtype,
+                                        self.bias_dtype, out_dtype, act)
+
+    def free(self) -> None:
+        if self.lin is not None:
+            self.ctx.q.linear_free(self.ctx.handle, ctypes.byref(self.lin))
+            self.lin = None
+            for b in (self.w_q, self.scales, self.biases, self.bias):
+                if b:
+                    b.handle = None
+
+
+def describe_linear(quant: "abi.QuantVtbl", path: str, prefix: str, group_size: int = 0,
+                    bits: int = 0) -> "abi.LinearInfo":
+    """Host-only header parse (no device needed): the layer's shapes and offsets."""
+    info = abi.LinearInfo()
+    _check(quant.linear_describe(path.encode(), prefix.encode(), group_size, bits, ctypes.byref(info)),
+           "linear_describe")
+    return info
 
 
 def esize(dtype: int) -> int:

@@ -189,6 +189,43 @@ def quantized_matmul(x, w_q, scales, biases, M: int, K: int, N: int, group_size:
     return y
 
 
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU = 0, 1, 2, 3
+
+
+def _erf(v: np.ndarray) -> np.ndarray:
+    from scipy.special import erf
+    return erf(v)
+
+
+def activation(v: np.ndarray, act: int) -> np.ndarray:
+    """The fused op's activations in float64 (no reference counterpart; the
+    plugin header lux_gpu_quant_backend.h defines them):
+    relu(v) = v < 0 ? 0 : v (NaN passes), silu(v) = v / (1 + exp(-v)),
+    gelu(v) = v/2 (1 + erf(v / sqrt 2))."""
+    v = np.asarray(v, np.float64)
+    if act == ACT_NONE:
+        return v
+    if act == ACT_RELU:
+        return np.where(v < 0, 0.0, v)
+    if act == ACT_SILU:
+        with np.errstate(over="ignore"):
+            return v / (1.0 + np.exp(-v))
+    if act == ACT_GELU:
+        return 0.5 * v * (1.0 + _erf(v / np.sqrt(2.0)))
+    raise ValueError(act)
+
+
+def fused_epilogue(acc: np.ndarray, bias, bias_dtype: int, act: int, out_dtype: int) -> np.ndarray:
+    """out = round_out(act(acc + bias[n])) for an fp32 accumulator [M, N]
+    (the oracle's quantized_matmul with out_dtype FLOAT32): the bias add in
+    fp32 as the kernels do it, the activation in float64, one rounding to
+    fp32 and then to out_dtype."""
+    v = np.asarray(acc, np.float32)
+    if bias is not None:
+        v = (v + to_f32(np.asarray(bias), bias_dtype)[None, :]).astype(np.float32)
+    return from_f32(activation(v, act).astype(np.float32), out_dtype)
+
+
 def check_args(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype) -> int:
     return lib().lux_cpu_quant_check(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype)
 

@@ -382,3 +382,78 @@ def test_config3_prefill_sampled(ctx, oracle, N):
         print(f"config3 N={N} out={od}: vs dequant-to-bf16 oracle {r:.3g}, vs exact-weight oracle {dev:.3g}")
         # bf16 weight rounding (2^-9 relative per weight) bounds the deviation
         assert dev < 8e-3
+
+
+# ---- fused output stage (bias + activation in the kernel's store) ---------
+
+FUSED_CASES = [
+    # M, K, N, bits, gs, x dtype: AUTO routes each to a different kernel
+    (1, 4096, 300, 4, 64, F16),     # stream GEMV
+    (6, 960, 70, 3, 64, F16),       # row-run GEMV (3-bit, K % 1024 != 0)
+    (6, 512, 96, 4, 64, BF16),      # skinny MFMA GEMV
+    (4, 4096, 64, 4, 64, BF16),     # decode MFMA kernel
+    (6, 2048, 40, 8, 128, F16),     # mid-M ring kernel (8-bit)
+    (32, 2048, 72, 4, 64, BF16),    # small-M GEMM
+    (96, 512, 136, 4, 64, F16),     # large GEMM
+    (3, 96, 20, 4, 32, F32),        # generic kernel (K % 64 != 0)
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: f"M{c[0]}K{c[1]}N{c[2]}b{c[3]}")
+@pytest.mark.parametrize("act", [0, 1, 2, 3], ids=["none", "relu", "silu", "gelu"])
+def test_fused_bias_activation(ctx, oracle, case, act):
+    """op_quantized_matmul_fused: out = act(x . w_hat^T + bias) with the
+    bias and activation applied in fp32 by the kernel that computes out,
+    against the oracle's fp32 matmul followed by the same stage; f32 output
+    at the fp32 gate, plus a bf16-output run at the bf16 gate."""
+    from mlx_amd import abi, runtime
+    O = oracle
+    M, K, N, bits, gs, xd = case
+    sbd = F16 if xd == F32 else xd
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=5000 + M + act)
+    bias_dt = [F32, F16, BF16, F32][act]
+    bias = O.from_f32(O.rng_normal(N, seed=6000 + N), bias_dt)
+    gemm = ctx.select_kernel(M, K, N, gs, bits, xd, sbd) == abi.KERNEL_GEMM
+    acc = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, F32,
+                             w_round=xd if gemm else F32)
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    bb = ctx.upload(bias)
+    try:
+        for od in (F32, BF16):
+            out = ctx.alloc(M * N * runtime.esize(od))
+            print(f"[case] fused M={M} K={K} N={N} b={bits} act={act} out={od}", flush=True)
+            ctx.quantized_matmul_fused(*bufs, bb, out, M, K, N, gs, bits, xd, sbd, bias_dt, od, act)
+            y = out.download(runtime.np_dtype(od), (M, N))
+            out.free()
+            check_output(O, y, O.fused_epilogue(acc, bias, bias_dt, act, od), od, f"fused act{act} out{od}")
+        # no bias: the same as the plain op followed by the activation
+        out = ctx.alloc(M * N * 4)
+        ctx.quantized_matmul_fused(*bufs, None, out, M, K, N, gs, bits, xd, sbd, F32, F32, act)
+        y = out.download(np.float32, (M, N))
+        out.free()
+        check_output(O, y, O.fused_epilogue(acc, None, F32, act, F32), F32, f"fused act{act} no bias")
+    finally:
+        for t in bufs + [bb]:
+            t.free()
+
+
+def test_fused_errors(ctx, oracle):
+    """Unknown activation, a short bias buffer: INVALID_ARGUMENT; a bias in
+    an unsupported dtype: NOT_SUPPORTED; nothing is launched."""
+    from mlx_amd import abi, runtime
+    O = oracle
+    M, K, N = 1, 256, 32
+    x, w_q, s, b, _ = O.make_problem(M, K, N, 4, 64, F16, F16, seed=7)
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    out, short, okb = ctx.alloc(M * N * 2), ctx.alloc(N * 2 - 2), ctx.alloc(N * 4)
+    try:
+        for bias, bdt, act, code in [(okb, F32, 4, abi.ERR_INVALID_ARGUMENT),
+                                     (okb, F32, -1, abi.ERR_INVALID_ARGUMENT),
+                                     (short, F16, 0, abi.ERR_INVALID_ARGUMENT),
+                                     (okb, 7, 0, abi.ERR_NOT_SUPPORTED)]:
+            with pytest.raises(runtime.LuxError) as e:
+                ctx.quantized_matmul_fused(*bufs, bias, out, M, K, N, 64, 4, F16, F16, bdt, F16, act)
+            assert e.value.code == code
+    finally:
+        for t in bufs + [out, short, okb]:
+            t.free()

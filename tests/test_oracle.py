@@ -338,3 +338,43 @@ def test_check_args(oracle):
     assert O.check_args(1, 4000, 4096, 64, 4, 0, 0, 0) == 1     # K % group
     assert O.check_args(1, 4096, 4096, 64, 4, 4, 0, 0) == 3     # dtype
     assert O.check_args(-1, 4096, 4096, 64, 4, 0, 0, 0) == 1
+
+
+# ------------------------------------------------------ fused output stage --
+
+def test_activation_closed_forms(oracle):
+    """The fused op's activations: exact identities and known values that a
+    dropped term, a wrong sign or a wrong constant fails."""
+    O = oracle
+    v = np.linspace(-8.0, 8.0, 4001)
+    for act in (O.ACT_SILU, O.ACT_GELU):
+        # f(v) - f(-v) = v for both (f(v) = v * c(v) with c(v) + c(-v) = 1)
+        assert np.allclose(O.activation(v, act) - O.activation(-v, act), v, rtol=0, atol=1e-12)
+        assert O.activation(np.array([0.0]), act)[0] == 0.0
+    # known values: silu(1) = 1 / (1 + e^-1), gelu(1) = Phi(1), gelu(-1) = -(1 - Phi(1))
+    assert abs(O.activation(np.array([1.0]), O.ACT_SILU)[0] - 0.7310585786300049) < 1e-15
+    assert abs(O.activation(np.array([1.0]), O.ACT_GELU)[0] - 0.8413447460685429) < 1e-15
+    assert abs(O.activation(np.array([-1.0]), O.ACT_GELU)[0] + 0.15865525393145707) < 1e-15
+    # large |v|: silu and gelu approach relu
+    big = np.array([-40.0, 40.0])
+    for act in (O.ACT_SILU, O.ACT_GELU):
+        assert np.allclose(O.activation(big, act), [0.0, 40.0], atol=1e-12)
+    r = O.activation(np.array([-2.0, -0.0, 0.0, 3.5, np.nan]), O.ACT_RELU)
+    assert r[0] == 0 and r[3] == 3.5 and np.isnan(r[4])
+    assert np.array_equal(O.activation(v, O.ACT_NONE), v)
+
+
+def test_fused_epilogue_bias_and_rounding(oracle):
+    """bias is added in fp32 per column; the result is rounded once to
+    fp32 and then to the output type."""
+    O = oracle
+    acc = np.array([[1.0, -2.0, 0.5], [3.0, 0.25, -7.0]], np.float32)
+    bias = O.from_f32(np.array([0.5, 1.0, -0.5], np.float32), O.F16)
+    got = O.fused_epilogue(acc, bias, O.F16, O.ACT_RELU, O.F32)
+    assert np.array_equal(got, np.array([[1.5, 0.0, 0.0], [3.5, 1.25, 0.0]], np.float32))
+    got = O.fused_epilogue(acc, None, O.F32, O.ACT_NONE, O.BF16)
+    assert np.array_equal(O.to_f32(got, O.BF16), acc)
+    # fp32 addition, not float64: 1 + 2^-30 rounds to 1
+    one = np.array([[1.0]], np.float32)
+    tiny = np.array([2.0 ** -30], np.float32)
+    assert O.fused_epilogue(one, tiny, O.F32, O.ACT_NONE, O.F32)[0, 0] == np.float32(1.0)
