@@ -3,9 +3,10 @@
 //
 // y[m, n] = sum_g s[n,g] * sum_{k in g} q[n,k] x[m,k] + b[n,g] * sum_{k in g} x[m,k]
 //
-// Work split: a block owns two 16-row tiles of W over the whole K; its K/1024
-// waves (at most 8) split K, 1024 codes each, and their partial sums meet in
-// LDS.  Every wave issues all its loads first -- the scales and biases of its
+// Work split: a block owns TILES 16-row tiles of W over the whole K; its
+// K/KW waves (at most 8) split K, KW codes each, and their partial sums meet
+// in LDS.  More tiles per block share each x operand (and the block's copy
+// of x) among more MFMAs and give each wave independent MFMA chains.  Every wave issues all its loads first -- the scales and biases of its
 // own row's groups, then per tile 8 weight loads of 128 bits per lane (W row
 // n0 + lane % 16, lane group c = lane / 16 reading bytes 16c .. 16c+15 of
 // each 64-byte quarter of a 256-code segment) -- and computes each segment
@@ -46,9 +47,6 @@ using skinny::mfma32;
 using skinny::u4;
 using skinny::x_operand;
 
-constexpr int kKW = 1024;         // codes of K per wave
-constexpr int kSegs = kKW / 256;  // 256-code segments per wave
-constexpr int kTiles = 2;         // 16-row tiles per block
 constexpr int kMaxM = 8;
 
 // Code operand v = 1 + q/kPow, exact in T: the 4-bit code sits in the top
@@ -117,27 +115,37 @@ __device__ __forceinline__ float sb_reg(const uint32_t* r, int g) {
     else return __uint_as_float(g & 1 ? r[g >> 1] & 0xffff0000u : r[g >> 1] << 16);
 }
 
-template <int GS, int SB>
+template <int GS, int SB, int KW>
 struct DGeo {
     static constexpr int kSb = SB == DT_F32 ? 4 : 2;
-    static constexpr int kGW = kKW / GS;                 // groups per wave
+    static constexpr int kGW = KW / GS;                  // groups per wave
     static constexpr int kSbWords = kGW * kSb / 4;       // scale dwords per row per wave
     static constexpr int kSbLoads = kSbWords / 4;        // 128-bit loads of them
-    static_assert(kSbWords % 4 == 0, "scale rows of a wave are whole 16-byte chunks");
+    static constexpr bool kFits = kSbWords % 4 == 0;   // scale rows of a wave are whole 16-byte chunks
 };
 
-// LDS: the M rows of x, then the partial sums of waves 1.. for the K reduction
-__host__ __device__ constexpr size_t dec_lds_bytes(int M, int K) {
-    return (size_t)M * (2 * K + 16) + (size_t)(K / kKW - 1) * kTiles * 4 * 64 * 4;
+// a block shape the kernel takes: whole 16-byte scale chunks per wave, and
+// every load of a wave (weights, scales, biases) countable by vmcnt
+template <int GS, int SB, int TILES, int KW>
+constexpr bool dec_ok() {
+    using Q = DGeo<GS, SB, KW>;
+    return Q::kFits && (KW / 256) * 2 * TILES + 2 * TILES * Q::kSbLoads < 64;
 }
 
-template <int TX, int SB, int GS, bool EPI>
+// LDS: the M rows of x, then the partial sums of waves 1.. for the K reduction
+__host__ __device__ constexpr size_t dec_lds_bytes(int M, int K, int tiles, int kw) {
+    return (size_t)M * (2 * K + 16) + (size_t)(K / kw - 1) * tiles * 4 * 64 * 4;
+}
+
+template <int TX, int SB, int GS, bool EPI, int TILES, int KW>
 __global__ __launch_bounds__(512) void qgemv_dec_kernel(const void* __restrict__ x, const uint32_t* __restrict__ wq,
                                                         const void* __restrict__ scales,
                                                         const void* __restrict__ biases, void* __restrict__ y,
                                                         int M, int K, int N, Epilogue ep) {
     using F = DForm<TX>;
-    using Q = DGeo<GS, SB>;
+    using Q = DGeo<GS, SB, KW>;
+    static_assert(dec_ok<GS, SB, TILES, KW>(), "block shape");
+    constexpr int kTiles = TILES, kKW = KW, kSegs = KW / 256;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

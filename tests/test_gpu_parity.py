@@ -457,3 +457,35 @@ def test_fused_errors(ctx, oracle):
     finally:
         for t in bufs + [out, short, okb]:
             t.free()
+
+
+@pytest.mark.parametrize("M,K,N,bits,gs,xd,sbd,kern", [
+    (96, 512, 136, 4, 64, BF16, BF16, "gemm"),   # large GEMM
+    (32, 1024, 70, 3, 32, F16, F32, "gemm"),     # small-M GEMM
+    (1, 4096, 96, 4, 64, F16, F16, "gemv"),      # stream GEMV
+    (4, 4096, 64, 4, 64, BF16, BF16, "gemv"),    # decode MFMA kernel
+    (8, 1024, 40, 8, 128, F16, F16, "gemv"),     # mid-M ring kernel
+    (3, 96, 20, 5, 32, F32, F32, "gemv"),        # generic kernel
+])
+def test_one_hot_rows_select_weight_columns(ctx, oracle, M, K, N, bits, gs, xd, sbd, kern):
+    """x row m = e_{k_m} (one 1.0, zeros elsewhere): y[m, :] is column k_m of
+    the dequantized weights.  The GEMM kernels round the weights to the
+    activation type first, so theirs is round_T(w_hat) bit for bit; the
+    GEMV kernels compute the exact form, within the fp32 gate."""
+    O = oracle
+    _, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=8000 + M)
+    ks = np.random.default_rng(M * K).integers(0, K, M)
+    xf = np.zeros((M, K), np.float32)
+    xf[np.arange(M), ks] = 1.0
+    x = O.from_f32(xf, xd)
+    y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, F32, KERNELS[kern])
+    if kern == "gemm":
+        w_t = O.to_f32(O.dequantize(w_q, s, b, K, gs, bits, sbd, xd), xd)
+        assert np.array_equal(y.view(np.uint32), np.ascontiguousarray(w_t[:, ks].T).view(np.uint32))
+    else:
+        w_hat = O.dequantize(w_q, s, b, K, gs, bits, sbd, F32)
+        check_output(O, y, np.ascontiguousarray(w_hat[:, ks].T), F32, f"one-hot {kern} M{M}")
+    # and x = 0 gives y = 0 on the same path
+    y0 = run(ctx, O.from_f32(np.zeros((M, K), np.float32), xd), w_q, s, b, M, K, N, gs, bits, xd, sbd, F32,
+             KERNELS[kern])
+    assert not np.any(y0)
