@@ -203,9 +203,10 @@ __device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, 
         issue_x(c, qx < nq ? qx : nq - 1);
     }
     // X(q) (and the older W(u)) landed: younger are the issues of steps
-    // q - kRX + 2 .. q: kRX - 1 x issues, plus a W issue for each of those
-    // steps that starts a super-step
-    constexpr int kYoung = (L::kRX - 1) * L::kNX + L::kNWS * (((P == 0) ? 1 : 0) + ((L::kRX == 3 && P == 1) ? 1 : 0));
+    // q - kRX + 2 .. q: kRX - 1 x issues, plus the W issue of the one of
+    // those steps that starts a super-step, if any (P <= kRX - 2; kRX <= 5)
+    static_assert(L::kRX >= 2 && L::kRX <= 5, "one W issue at most among the younger steps");
+    constexpr int kYoung = (L::kRX - 1) * L::kNX + L::kNWS * (P <= L::kRX - 2 ? 1 : 0);
     wait_vmcnt_small<kYoung>();
     const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
     // x fragments

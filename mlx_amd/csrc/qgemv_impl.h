@@ -501,8 +501,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
     const int nb0 = blockIdx.x * L::kRows;
     const int n0 = nb0 + wave * R;
 
+    // Weight and scale buffer resources start at the block's first row (its
+    // scales at the 16-byte chunk holding them), so every offset below stays
+    // far under 2^31 whatever N is; the zero-reading offset kZeroOff lies
+    // past every resource's size.
+    const size_t sb_first = (size_t)nb0 * sb_row;
+    const uint32_t sb_lead = (uint32_t)(sb_first & 15u);  // row nb0's scales within their chunk
+    const size_t sb_base = sb_first - sb_lead;
+
     // ---- 1. x rows (zeros past K and past M) and the block's scale/bias rows into LDS ----
-    const uint32_t sb_first = (uint32_t)nb0 * sb_row, sb_base = sb_first & ~15u;
     {
         const auto xr = buf_rsrc(x, (uint32_t)M * K * XE);
         constexpr int XC = MR * L::kXRow / 16;  // 16-byte chunks
@@ -519,12 +526,14 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(lds + L::X + cw * 16), 16, voff, 0, 0, 0);
         }
         // whole 16-byte chunks: the last one may run into the buffer's tail slack
-        const uint32_t sbytes = ((uint32_t)N * sb_row + 15u) & ~15u;
-        const auto sr = buf_rsrc(scales, sbytes), br = buf_rsrc(biases, sbytes);
-        const int sc = (int)((sb_first - sb_base + L::kRows * sb_row + 15) / 16);
+        const size_t sleft = (((size_t)N * sb_row - sb_base) + 15u) & ~(size_t)15u;
+        const uint32_t sbytes = (uint32_t)(sleft < 0x7fffffffu ? sleft : 0x7fffffffu);
+        const auto sr = buf_rsrc(static_cast<const uint8_t*>(scales) + sb_base, sbytes);
+        const auto br = buf_rsrc(static_cast<const uint8_t*>(biases) + sb_base, sbytes);
+        const int sc = (int)((sb_lead + L::kRows * sb_row + 15) / 16);
         for (int cw = wave * 64; cw < sc; cw += 64 * kStreamWaves) {
             if (cw + lane < sc) {
-                const uint32_t voff = sb_base + (uint32_t)(cw + lane) * 16;
+                const uint32_t voff = (uint32_t)(cw + lane) * 16;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_ptr)(lds + L::S + cw * 16), 16, voff, 0, 0, 0);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_ptr)(lds + L::B + cw * 16), 16, voff, 0, 0, 0);
             }
@@ -536,12 +545,14 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
     // (never stored), idle lanes read zeros ----
     uint32_t w[R][W];
     {
-        const auto wr = buf_rsrc(wq, (uint32_t)N * row_bytes);
+        const size_t wleft = (size_t)(N - nb0) * row_bytes;
+        const auto wr = buf_rsrc(reinterpret_cast<const uint8_t*>(wq) + (size_t)nb0 * row_bytes,
+                                 (uint32_t)(wleft < 0x7fffffffu ? wleft : 0x7fffffffu));
         const uint32_t voff = active ? (uint32_t)lane * (8 * BITS) : kZeroOff;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int n = n0 + r < N ? n0 + r : N - 1;
-            load_unit_buf<BITS>(wr, voff, (uint32_t)n * row_bytes, w[r]);
+            load_unit_buf<BITS>(wr, voff, (uint32_t)(n - nb0) * row_bytes, w[r]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -563,8 +574,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
     // ---- 5. rows in arrival order ----
     // the unit's first group (codes 64u..): group size 32 -> 2u (and 2u+1)
     const int g0 = (u << 6) >> gshift;
-    const uint8_t* ls = lds + L::S + (sb_first - sb_base) + (size_t)(wave * R) * sb_row + g0 * L::kSb;
-    const uint8_t* lb = lds + L::B + (sb_first - sb_base) + (size_t)(wave * R) * sb_row + g0 * L::kSb;
+    const uint8_t* ls = lds + L::S + sb_lead + (size_t)(wave * R) * sb_row + g0 * L::kSb;
+    const uint8_t* lb = lds + L::B + sb_lead + (size_t)(wave * R) * sb_row + g0 * L::kSb;
     constexpr int V = R * MR, VP = (V + 7) / 8 * 8;
     float acc[VP];
 #pragma unroll

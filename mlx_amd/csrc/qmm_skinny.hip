@@ -71,6 +71,9 @@ LuxStatus launch_sb(const QmmArgs& a, hipStream_t st) {
 LuxStatus launch_qmm_skinny(const QmmArgs& a, hipStream_t st) {
     using namespace skinny;
     if (a.M < 2 || a.M > 16 || (a.bits != 4 && a.bits != 8) || a.x_dtype == DT_F32) return LuxStatus::NotSupported;
+    // 32-bit buffer offsets (the scale arrays are smaller than the codes)
+    if ((size_t)a.M * a.K * 2 >= (1ull << 31) || (size_t)a.N * a.K * a.bits / 8 >= (1ull << 31))
+        return LuxStatus::NotSupported;
     if (a.bits == 4) return a.x_dtype == DT_F16 ? launch_sb<4, DT_F16>(a, st) : launch_sb<4, DT_BF16>(a, st);
     return a.x_dtype == DT_F16 ? launch_sb<8, DT_F16>(a, st) : launch_sb<8, DT_BF16>(a, st);
 }

@@ -489,3 +489,39 @@ def test_one_hot_rows_select_weight_columns(ctx, oracle, M, K, N, bits, gs, xd, 
     y0 = run(ctx, O.from_f32(np.zeros((M, K), np.float32), xd), w_q, s, b, M, K, N, gs, bits, xd, sbd, F32,
              KERNELS[kern])
     assert not np.any(y0)
+
+
+def test_weights_past_2gib(ctx, oracle):
+    """Packed weights larger than 2^31 bytes (K=4096, 4-bit, 1 052 675 rows:
+    2 GiB + 8 MB): the GEMV kernels address them with per-block buffer
+    bases, the size-limited kernels decline them, and every sampled row --
+    the first ones, rows around the 2^31-byte mark, the last block -- equals
+    the oracle for M = 1 and 3 (stream kernel) and 6 (row-run kernel)."""
+    O = oracle
+    K, gs, bits = 4096, 64, 4
+    N = (1 << 31) // (K // 2) + 4099
+    rng = np.random.default_rng(11)
+    w_q = rng.integers(0, 2**32, size=(N, K * bits // 32), dtype=np.uint32)
+    G = K // gs
+    s = O.from_f32(rng.uniform(0.001, 0.02, size=(N, G)).astype(np.float32), F16)
+    b = O.from_f32(rng.uniform(-0.1, 0.0, size=(N, G)).astype(np.float32), F16)
+    mark = (1 << 31) // (K // 2)
+    rows = np.unique(np.concatenate([np.arange(64), np.arange(mark - 40, mark + 40),
+                                     rng.integers(0, N, 200), np.arange(N - 70, N)]))
+    from mlx_amd import runtime
+    bufs = [ctx.upload(a) for a in (w_q, s, b)]
+    try:
+        for M in (1, 3, 6):
+            x = O.from_f32(O.rng_normal(M * K, 900 + M).reshape(M, K), F16)
+            X, Y = ctx.upload(x), ctx.alloc(M * N * 4)
+            print(f"[case] qmm M={M} K={K} N={N} (weights {w_q.nbytes} B)", flush=True)
+            ctx.quantized_matmul(X, *bufs, Y, M, K, N, gs, bits, F16, F16, F32)
+            y = Y.download(np.float32, (M, N))
+            X.free()
+            Y.free()
+            want = O.quantized_matmul(x, w_q[rows], s[rows], b[rows], M, K, len(rows), gs, bits, F16, F16, F32)
+            check_output(O, np.ascontiguousarray(y[:, rows]), want, F32, f"2 GiB weights M{M}")
+            assert np.all(np.isfinite(y))
+    finally:
+        for t in bufs:
+            t.free()
