@@ -496,7 +496,8 @@ def test_weights_past_2gib(ctx, oracle):
     2 GiB + 8 MB): the GEMV kernels address them with per-block buffer
     bases, the size-limited kernels decline them, and every sampled row --
     the first ones, rows around the 2^31-byte mark, the last block -- equals
-    the oracle for M = 1 and 3 (stream kernel) and 6 (row-run kernel)."""
+    the oracle for M = 1 and 3 (stream kernel), 6 (row-run kernel) and 96
+    (the large GEMM, whose 32-bit offsets reach 4 GiB)."""
     O = oracle
     K, gs, bits = 4096, 64, 4
     N = (1 << 31) // (K // 2) + 4099
@@ -508,10 +509,10 @@ def test_weights_past_2gib(ctx, oracle):
     mark = (1 << 31) // (K // 2)
     rows = np.unique(np.concatenate([np.arange(64), np.arange(mark - 40, mark + 40),
                                      rng.integers(0, N, 200), np.arange(N - 70, N)]))
-    from mlx_amd import runtime
+    from mlx_amd import abi
     bufs = [ctx.upload(a) for a in (w_q, s, b)]
     try:
-        for M in (1, 3, 6):
+        for M in (1, 3, 6, 96):
             x = O.from_f32(O.rng_normal(M * K, 900 + M).reshape(M, K), F16)
             X, Y = ctx.upload(x), ctx.alloc(M * N * 4)
             print(f"[case] qmm M={M} K={K} N={N} (weights {w_q.nbytes} B)", flush=True)
@@ -519,7 +520,10 @@ def test_weights_past_2gib(ctx, oracle):
             y = Y.download(np.float32, (M, N))
             X.free()
             Y.free()
-            want = O.quantized_matmul(x, w_q[rows], s[rows], b[rows], M, K, len(rows), gs, bits, F16, F16, F32)
+            gemm = ctx.select_kernel(M, K, N, gs, bits, F16) == abi.KERNEL_GEMM
+            assert gemm == (M > 8)
+            want = O.quantized_matmul(x, w_q[rows], s[rows], b[rows], M, K, len(rows), gs, bits, F16, F16, F32,
+                                      variant="omp", w_round=F16 if gemm else F32)
             check_output(O, np.ascontiguousarray(y[:, rows]), want, F32, f"2 GiB weights M{M}")
             assert np.all(np.isfinite(y))
     finally:
