@@ -4,7 +4,8 @@ The plugin is compiled from mlx_amd/csrc/*.hip (hipcc, gfx950) and the
 host-only mlx_amd/csrc/*.cpp (g++) into mlx_amd/lib/.  Every
 source is compiled each time build() runs (the driver's "does it build"
 check); objects land in mlx_amd/_build/ and are linked into one shared
-library whose only exported symbols are the two plugin entry points.
+library whose only exported symbols are the two plugin entry points;
+csrc/core/lux_quant_core.cpp builds the separate core-side library.
 """
 from __future__ import annotations
 
@@ -19,6 +20,8 @@ CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIBDIR = os.path.join(PKG, "lib")
 PLUGIN = os.path.join(LIBDIR, "libluxgpu_backend_hip.so")
+CORE = os.path.join(LIBDIR, "libluxgpu_quant_core.so")
+CORE_SRC = os.path.join(CSRC, "core", "lux_quant_core.cpp")
 ARCH = os.environ.get("LUX_HIP_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -66,9 +69,22 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, PLUGIN)
+    build_core()
     if verbose:
-        print(f"built {PLUGIN}", file=sys.stderr)
+        print(f"built {PLUGIN} and {CORE}", file=sys.stderr)
     return PLUGIN
+
+
+def build_core() -> str:
+    """The core-side selection library: host C++ only, linked with libdl."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    tmp = CORE + ".tmp"
+    cmd = [CXX, *CXXFLAGS, "-shared", CORE_SRC, "-ldl", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"core library build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CORE)
+    return CORE
 
 
 if __name__ == "__main__":

@@ -11,7 +11,7 @@ Mirrors reference src/plugin_loader.hpp:
     symbol, call it; init false => registered unavailable; ABI mismatch =>
     message on stderr, library closed, rejected (:184-232);
   * get_best_backend: priority metal, cuda, webgpu (:250-262), extended with
-    hip.
+    hip ahead of webgpu (a native GPU backend before the portable one).
 and adds what the reference documents but does not implement
 (README.md:65): LUX_BACKEND=<name> selects a backend explicitly.  After a
 plugin is accepted, the optional quant extension symbol is looked up.
@@ -27,7 +27,7 @@ from typing import Dict, List, Optional
 from . import abi
 
 PKG_LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
-PRIORITY = ("metal", "cuda", "webgpu", "hip")
+PRIORITY = ("metal", "cuda", "hip", "webgpu")
 
 try:
     from _ctypes import dlclose as _dlclose

@@ -22,18 +22,21 @@ def _run(cmd, **kw):
     return r.stdout
 
 
-def declared_symbols():
-    """Functions the public headers declare with default visibility."""
+PLUGIN_HEADERS = ("lux_gpu_backend_abi.h", "lux_gpu_quant_backend.h")
+CORE_HEADERS = ("lux_quant_core.h",)
+
+
+def declared_symbols(headers=PLUGIN_HEADERS):
+    """Functions the given public headers declare with default visibility."""
     syms = set()
-    for h in os.listdir(INCLUDE):
-        if h.endswith(".h"):
-            txt = open(os.path.join(INCLUDE, h)).read()
-            syms |= set(re.findall(r'visibility\("default"\)\)\)\s+\w+\s+(\w+)\s*\(', txt))
+    for h in headers:
+        txt = open(os.path.join(INCLUDE, h)).read()
+        syms |= set(re.findall(r'visibility\("default"\)\)\)\s+[\w ]+?\**\s*\**(\w+)\s*\(', txt))
     return syms
 
 
 def test_headers_compile_and_layout_asserts_hold(tmp_path):
-    for h in ("lux_gpu_backend_abi.h", "lux_gpu_quant_backend.h"):
+    for h in PLUGIN_HEADERS + CORE_HEADERS:
         src = tmp_path / "t.c"
         src.write_text(f'#include "{INCLUDE}/{h}"\nint main(void){{return 0;}}\n')
         _run(["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", str(src)])
@@ -78,6 +81,19 @@ def test_plugin_exports_exactly_the_declared_symbols():
     assert {s for s in exported if s.startswith("lux")} == declared
     # and the library loads; its symbols resolve through dlsym
     lib = ctypes.CDLL(mlx_amd.PLUGIN_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    for s in declared:
+        assert getattr(lib, s) is not None
+
+
+def test_core_library_exports_exactly_the_declared_symbols():
+    import mlx_amd
+    assert os.path.exists(mlx_amd.CORE_PATH), "run __graft_entry__.build() first"
+    out = _run(["nm", "-D", "--defined-only", mlx_amd.CORE_PATH])
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    declared = declared_symbols(CORE_HEADERS)
+    assert len(declared) == 12 and "lux_tensor_quantized_matmul" in declared
+    assert {s for s in exported if s.startswith("lux")} == declared
+    lib = ctypes.CDLL(mlx_amd.CORE_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
     for s in declared:
         assert getattr(lib, s) is not None
 
