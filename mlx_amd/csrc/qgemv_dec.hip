@@ -17,13 +17,11 @@ LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     const size_t lds = dec_lds_bytes(a.M, a.K, TILES, KW);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
     auto kern = qgemv_dec_kernel<TX, SB, GS, EPI, TILES, KW>;
-    static bool attr_set = false;  // one per instantiation
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024) != hipSuccess)
-            return LuxStatus::Internal;
-        attr_set = true;
-    }
+    // once per instantiation; a function-local static initializes exactly once
+    // even when several threads make the first call together
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return LuxStatus::Internal;
     const int blocks = (a.N + 16 * TILES - 1) / (16 * TILES);
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * (a.K / KW)), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.M,
                        a.K, a.N, a.epi());

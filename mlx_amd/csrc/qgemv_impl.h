@@ -670,13 +670,11 @@ LuxStatus launch_t_e(const QmmArgs& a, hipStream_t st) {
     const int waves = (a.N + rpw - 1) / rpw;
     const int blocks = (waves + 3) / 4;
     auto kern = qgemv_kernel<BITS, TX, MR, RU, EPI>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024) != hipSuccess)
-            return LuxStatus::Internal;
-        attr_set = true;
-    }
+    // once per instantiation; a function-local static initializes exactly once
+    // even when several threads make the first call together
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+    if (attr != hipSuccess) return LuxStatus::Internal;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a.x, a.wq, a.scales, a.biases,
                        a.y, a.M, a.K, a.N, a.group_size, a.sb_dtype, a.epi(), rpw);
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;

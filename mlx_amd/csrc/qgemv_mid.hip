@@ -9,13 +9,11 @@ LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     using L = Lay<BITS, SB, GS, XR>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
     auto kern = qgemv_mid_kernel<BITS, TX, SB, GS, XR, EPI>;
-    static bool attr_set = false;  // one per instantiation
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                L::kBytes) != hipSuccess)
-            return LuxStatus::Internal;
-        attr_set = true;
-    }
+    // once per instantiation; a function-local static initializes exactly once
+    // even when several threads make the first call together
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+    if (attr != hipSuccess) return LuxStatus::Internal;
     hipLaunchKernelGGL(kern, dim3((a.N + 31) / 32), dim3(64 * kWaves), L::kBytes, st, a.x, a.wq, a.scales, a.biases,
                        a.y, a.M, a.K, a.N, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;

@@ -11,13 +11,11 @@ LuxStatus launch_e(const QmmArgs& a, int KS, hipStream_t st) {
     const size_t lds = skinny_lds_bytes(a.M, a.K, a.K / GS, kSb, tiles);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
     auto kern = qmm_skinny_kernel<BITS, TX, SB, GS, GW, EPI>;
-    static bool attr_set = false;  // one per instantiation
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024) != hipSuccess)
-            return LuxStatus::Internal;
-        attr_set = true;
-    }
+    // once per instantiation; a function-local static initializes exactly once
+    // even when several threads make the first call together
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return LuxStatus::Internal;
     const int rows = 16 * tiles;
     const int blocks = (a.N + rows - 1) / rows;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * kWaves), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.M,

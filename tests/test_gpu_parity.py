@@ -529,3 +529,44 @@ def test_weights_past_2gib(ctx, oracle):
     finally:
         for t in bufs:
             t.free()
+
+
+def test_two_contexts_on_two_threads(oracle):
+    """Independent contexts, one caller thread each (the plugin contract):
+    both threads run several kernel families at once (ctypes releases the
+    GIL around every plugin call) and each result equals the oracle."""
+    import threading
+    from mlx_amd import runtime
+    O = oracle
+    cases = [(1, 4096, 2048, 4, 64, F16), (4, 2048, 512, 4, 32, BF16), (32, 2048, 256, 8, 128, BF16),
+             (6, 512, 300, 3, 64, F16), (128, 512, 256, 4, 64, F16)]
+    problems = [O.make_problem(M, K, N, b, g, xd, xd, seed=9000 + i) for i, (M, K, N, b, g, xd) in enumerate(cases)]
+    results, errors = {}, []
+
+    def worker(tid):
+        try:
+            with runtime.Context(0) as c:
+                for rep in range(3):
+                    for i, ((M, K, N, b, g, xd), (x, w_q, s, bb, _)) in enumerate(zip(cases, problems)):
+                        y = runtime.run_quantized_matmul(c, x, w_q, s, bb, M, K, N, g, b, xd, xd, F32)
+                        results[(tid, rep, i)] = y
+        except Exception as e:  # reported below, on the main thread
+            errors.append(repr(e))
+
+    ts = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert all(not t.is_alive() for t in ts)
+    ctx = runtime.Context(0)
+    try:
+        for i, ((M, K, N, b, g, xd), (x, w_q, s, bb, _)) in enumerate(zip(cases, problems)):
+            gemm = ctx.select_kernel(M, K, N, g, b, xd) == 2
+            want = O.quantized_matmul(x, w_q, s, bb, M, K, N, g, b, xd, xd, F32, w_round=xd if gemm else F32)
+            for tid in range(2):
+                for rep in range(3):
+                    check_output(O, results[(tid, rep, i)], want, F32, f"thread {tid} rep {rep} case {i}")
+    finally:
+        ctx.close()
