@@ -118,6 +118,21 @@ __device__ __forceinline__ void dma4(uint32_t m0v, const void* sbase, uint32_t v
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// W rows of a super-step slot are 32*BITS bytes = 2*BITS 16-byte chunks.
+// Where that count is a power of two (BITS 2, 4, 8) chunk c of row r sits at
+// position c ^ wswz(r) (through the DMA source address, like x): the row
+// stride is a multiple of 64 B (256 B for 8-bit codes, a whole bank cycle),
+// so without it the 32 lanes reading 32 rows' codes hit the same banks
+// (measured at c2: 3.9M conflict cycles against 0.3M active LDS cycles).
+// 16 consecutive rows reading one chunk then cover 16 distinct 16-byte slots
+// of a 256-byte bank window.
+template <int BITS>
+__device__ __forceinline__ int wswz(int r) {
+    constexpr int kCpr = 2 * BITS;
+    if constexpr ((kCpr & (kCpr - 1)) == 0 && kCpr <= 16) return (r / (16 / kCpr)) & (kCpr - 1);
+    else return 0;
+}
+
 template <int BITS, int SB, int MT, int GS>
 struct Lay {
     static constexpr int kSb = SB == DT_F32 ? 4 : 2;
@@ -220,10 +235,14 @@ __device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, 
     }
     // codes and scale of this lane's 32 codes
     const int slot = u % L::kRW;
-    const uint32_t* wc = reinterpret_cast<const uint32_t*>(lw + L::kW0 + slot * L::kWS + j * 32 * BITS + P * 8 * BITS + 4 * BITS * h);
+    const uint8_t* wrow = lw + L::kW0 + slot * L::kWS + j * 32 * BITS;
+    const int wz = wswz<BITS>(j);
     uint32_t cw[BITS];
 #pragma unroll
-    for (int i = 0; i < BITS; i++) cw[i] = wc[i];
+    for (int i = 0; i < BITS; i++) {
+        const int byte = P * 8 * BITS + 4 * BITS * h + 4 * i;  // within the row, before the swizzle
+        cw[i] = *reinterpret_cast<const uint32_t*>(wrow + ((((byte >> 4) ^ wz) << 4) | (byte & 15)));
+    }
     const int gi = (P * 64 + 32 * h) / GS;
     const uint8_t* sp = lw + L::kS0 + slot * L::kSS + j * L::kSPR + gi * L::kSb;
     const uint8_t* bp = lw + L::kB0 + slot * L::kSS + j * L::kSPR + gi * L::kSb;
@@ -271,7 +290,7 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     for (int i = 0; i < BITS; i++) {
         const int v = 64 * i + lane, r = v / (2 * BITS), ch = v % (2 * BITS);
         const int n = n0 + r < N ? n0 + r : N - 1;
-        c.woff[i] = (uint32_t)n * row_bytes + 16u * ch;
+        c.woff[i] = (uint32_t)n * row_bytes + 16u * (ch ^ wswz<BITS>(r));  // lands at position ch
     }
 #pragma unroll
     for (int i = 0; i < L::kNS; i++) {
