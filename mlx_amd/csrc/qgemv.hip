@@ -15,12 +15,16 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
     // 2..16 rows of x: the MFMA kernels where they apply (16-bit x; the
     // decode kernel takes 4-bit codes and M <= 8, the LDS-ring kernel 4/8-bit
-    // codes; both need K % 1024 == 0)
-    if (args.M >= 2 && args.M <= 8) {
+    // codes; both need K % 1024 == 0).  Two rows of 16-bit x with K <= 4096
+    // run faster on the stream kernel (4-bit, graph replays: 11.1 us against
+    // 11.5 at K = 4096, N = 14336; 8.0 against 11.0 at N = 11008; 4.9
+    // against 5.9 at N = 4096).
+    const bool stream2 = args.M == 2 && args.K <= 4096 && args.x_dtype != DT_F32;
+    if (args.M >= 2 && args.M <= 8 && !stream2) {
         const LuxStatus s = launch_qgemv_dec(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
-    if (args.M >= 2 && args.M <= 16) {
+    if (args.M >= 2 && args.M <= 16 && !stream2) {
         const LuxStatus s = launch_qgemv_mid(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }

@@ -4,16 +4,21 @@
 namespace lxq {
 namespace dec {
 
-// block shape: 16-row tiles per block, and codes of K per wave (kDecKW512:
-// 512 where the wave count K/512 stays within 8 and the shape fits, else
-// 1024).  Measured at c1 (K = 4096, N = 14336), M = 2 / 4 / 8: 2 tiles x
-// 1024 codes 11.5-11.9 / 12.1-12.4 / 12.5 us; 2 x 512 12.0 / 12.5-12.8 /
-// 13.2; 4 x 1024 14.9 / 15.3-15.4 / 15.6; 4 x 512 14.5 / 14.7 / 15.1.
-constexpr int kDecTiles = 2;
-constexpr bool kDecKW512 = false;
+// Block shape: 1024 codes of K per wave; 2 16-row tiles per block (their
+// MFMAs share each x operand), or 1 where 2-tile blocks would leave CUs
+// without a block and every 1-tile block is resident at once.  Measured
+// (graph replays, us), M = 2 / 4 / 8:
+//   K = 4096, N = 14336: 2 tiles 11.5 / 12.3 / 13.0, 1 tile 11.7 / 13.0 / 15.5;
+//     2 x 512 codes 12.0 / 12.5-12.8 / 13.2; 4 tiles 14.9 / 15.3 / 15.6
+//   K = 4096, N = 4096 (128 2-tile blocks): 2 tiles 7.4 / 7.8 / 8.0, 1 tile 5.9 / 6.2 / 6.4
+//   K = 8192, N = 8192, M = 4 / 8: 2 tiles 16.3 / 16.9, 1 tile 14.8 / 19.0
+//     (at M = 8 one 1-tile block fills a CU's LDS: the 512 blocks run in two rounds)
+constexpr int kCUs = 256;           // gfx950 (MI355X)
+constexpr int kWavesPerCU1 = 20;    // 1-tile kernel: <= 96 VGPRs, 5 waves per SIMD
 
-template <int TX, int SB, int GS, bool EPI, int TILES, int KW>
+template <int TX, int SB, int GS, bool EPI, int TILES>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
+    constexpr int KW = 1024;
     const size_t lds = dec_lds_bytes(a.M, a.K, TILES, KW);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
     auto kern = qgemv_dec_kernel<TX, SB, GS, EPI, TILES, KW>;
@@ -30,11 +35,14 @@ LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
 
 template <int TX, int SB, int GS, bool EPI>
 LuxStatus launch_kw(const QmmArgs& a, hipStream_t st) {
-    if constexpr (kDecKW512 && dec_ok<GS, SB, kDecTiles, 512>()) {
-        if (a.K / 512 <= 8) return launch_e<TX, SB, GS, EPI, kDecTiles, 512>(a, st);
-    }
-    if constexpr (dec_ok<GS, SB, kDecTiles, 1024>()) return launch_e<TX, SB, GS, EPI, kDecTiles, 1024>(a, st);
-    else return launch_e<TX, SB, GS, EPI, 2, 1024>(a, st);
+    static_assert(dec_ok<GS, SB, 1, 1024>() && dec_ok<GS, SB, 2, 1024>(), "block shapes");
+    const long b2 = (a.N + 31) / 32, b1 = (a.N + 15) / 16;
+    const size_t lds1 = dec_lds_bytes(a.M, a.K, 1, 1024);
+    const long lds_fit = lds1 <= 160 * 1024 ? (long)(160 * 1024 / lds1) : 0;
+    const long wave_fit = kWavesPerCU1 / (a.K / 1024);
+    const long per_cu = lds_fit < wave_fit ? lds_fit : wave_fit;
+    if (b2 <= kCUs && b1 <= per_cu * kCUs) return launch_e<TX, SB, GS, EPI, 1>(a, st);
+    return launch_e<TX, SB, GS, EPI, 2>(a, st);
 }
 
 template <int TX, int SB, int GS>

@@ -107,10 +107,11 @@ def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
-    """2 <= M <= 16 with 4/8-bit codes runs an MFMA kernel (for K % 1024 == 0
+    """3 <= M <= 16 with 4/8-bit codes runs an MFMA kernel (for K % 1024 == 0
     the decode kernel at M <= 8 with 4-bit codes, else the LDS-ring one; the
     skinny one for other K): every group size, one and two x DMAs per step,
-    row tails in the 16-row tile and in the 32-column block."""
+    row tails in the 16-row tile and in the 32-column block.  M = 2 with
+    K <= 4096 runs the stream kernel."""
     O = oracle
     for (M, K, N, gs) in [(2, 1024, 77, 32), (4, 2048, 50, 64), (5, 1024, 77, 32), (8, 2048, 50, 64),
                           (16, 4096, 40, 128), (6, 4096, 33, 64), (12, 4096, 21, 32), (3, 3072, 65, 128),
@@ -125,16 +126,32 @@ def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
                                        (F16, BF16, F32), (BF16, F32, BF16)])
 def test_decode_mfma_parity(ctx, oracle, xd, sbd, od):
     """2 <= M <= 8 with 4-bit codes and K % 1024 == 0 runs the MFMA decode
-    kernel: every group size (all three lane regroupings), one to eight K
-    waves, N not a multiple of the 32-row block, M at both ends.  f32 scales
-    with group size 32 fall back to the LDS-ring kernel."""
+    kernel (M = 2 only for K > 4096): every group size (all three lane
+    regroupings), one to eight K waves, N not a multiple of the 32-row block,
+    M at both ends.  f32 scales with group size 32 fall back to the LDS-ring
+    kernel."""
     O = oracle
-    for (M, K, N, gs) in [(2, 1024, 45, 64), (8, 4096, 100, 64), (3, 2048, 77, 32), (7, 8192, 33, 128),
+    for (M, K, N, gs) in [(2, 6144, 45, 64), (8, 4096, 100, 64), (3, 2048, 77, 32), (7, 8192, 33, 128),
                           (4, 4096, 64, 32), (6, 3072, 19, 128), (5, 1024, 128, 64), (8, 8192, 50, 32)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, 4, gs, xd, sbd, seed=11 * M + gs)
         y = run(ctx, x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od, KERNELS["gemv"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od)
         check_output(O, y, want, od, f"decode M{M} K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_decode_block_shapes(ctx, oracle, xd, sbd, od):
+    """The decode launcher's two block shapes: 2-tile blocks when N/32 > 256
+    (N = 8208 and 8200: a half-empty last tile and a partly empty one), or
+    when the 1-tile blocks would not all be resident (M = 8, K = 8192: one
+    block fills a CU's LDS); 1-tile blocks otherwise (N = 8192, M = 4,
+    K = 8192: 512 blocks of 8 waves, two per CU)."""
+    O = oracle
+    for (M, K, N, gs) in [(3, 1024, 8208, 32), (8, 2048, 8200, 64), (8, 8192, 8192, 128), (4, 8192, 8192, 64)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, 4, gs, xd, sbd, seed=13 * M + gs)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od, KERNELS["gemv"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od, variant="omp")
+        check_output(O, y, want, od, f"decode blocks M{M} K{K} N{N} g{gs}")
 
 
 def test_gemv_is_deterministic(ctx, oracle):
