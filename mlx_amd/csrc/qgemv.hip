@@ -15,16 +15,21 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
     // 2..16 rows of x: the MFMA kernels where they apply (16-bit x; the
     // decode kernel takes 4-bit codes and M <= 8, the LDS-ring kernel 4/8-bit
-    // codes; both need K % 1024 == 0).  Two rows of 16-bit x with K <= 4096
-    // run faster on the stream kernel (4-bit, graph replays: 11.1 us against
-    // 11.5 at K = 4096, N = 14336; 8.0 against 11.0 at N = 11008; 4.9
-    // against 5.9 at N = 4096).
+    // codes; both need K % 1024 == 0), except where the stream kernel (M <= 4,
+    // K <= 4096) or the skinny one measured faster (graph replays):
+    //  - M = 2, 16-bit x, K <= 4096: 4-bit 11.1 us against 11.5 at K = 4096,
+    //    N = 14336; 8.0 against 11.0 at N = 11008; 4.9 against 5.9 at N = 4096;
+    //  - 8-bit codes, M <= 8, K <= 4096 (LDS-ring kernel skipped): M = 3 / 4 /
+    //    6 / 8 at K = 4096, N = 14336: 18.1 / 19.5 / 19.9 / 20.1 us against
+    //    22.7 / 22.9 / 23.1 / 23.2; M = 4, N = 4096: 7.2 against 10.5 (at
+    //    K = 8192 the LDS-ring kernel stays: 20.2 against 25.0).
     const bool stream2 = args.M == 2 && args.K <= 4096 && args.x_dtype != DT_F32;
+    const bool ring8 = !(args.bits == 8 && args.M <= 8 && args.K <= 4096);
     if (args.M >= 2 && args.M <= 8 && !stream2) {
         const LuxStatus s = launch_qgemv_dec(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
-    if (args.M >= 2 && args.M <= 16 && !stream2) {
+    if (args.M >= 2 && args.M <= 16 && !stream2 && ring8) {
         const LuxStatus s = launch_qgemv_mid(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }

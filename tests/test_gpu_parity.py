@@ -107,13 +107,16 @@ def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
-    """3 <= M <= 16 with 4/8-bit codes runs an MFMA kernel (for K % 1024 == 0
+    """2 <= M <= 16 with 4/8-bit codes: the MFMA kernels (for K % 1024 == 0
     the decode kernel at M <= 8 with 4-bit codes, else the LDS-ring one; the
-    skinny one for other K): every group size, one and two x DMAs per step,
-    row tails in the 16-row tile and in the 32-column block.  M = 2 with
-    K <= 4096 runs the stream kernel."""
+    skinny one for other K), and the launcher's exceptions to them: M = 2
+    with K <= 4096 runs the stream kernel, 8-bit codes with M <= 8 and
+    K <= 4096 the stream (M <= 4) or skinny kernels (the LDS-ring kernel
+    keeps M = 4, K = 6144).  Every group size, one and two x DMAs per step,
+    row tails in the 16-row tile and in the 32-column block."""
     O = oracle
     for (M, K, N, gs) in [(2, 1024, 77, 32), (4, 2048, 50, 64), (5, 1024, 77, 32), (8, 2048, 50, 64),
+                          (4, 6144, 37, 64),
                           (16, 4096, 40, 128), (6, 4096, 33, 64), (12, 4096, 21, 32), (3, 3072, 65, 128),
                           (9, 1024, 96, 64), (7, 512, 40, 64), (10, 256, 19, 32)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 7 + M)
