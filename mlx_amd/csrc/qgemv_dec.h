@@ -32,6 +32,10 @@
 // x is copied into LDS by buffer->LDS DMA before the weight loads (rows of
 // 2K + 16 bytes: the 16 rows an A-operand read touches fall in different bank
 // groups), so the one vmcnt wait for it leaves every weight load in flight.
+// With xw = 0 the block's waves copy x together and a barrier publishes it;
+// with xw = 1 each wave copies only its own K part, and its vmcnt wait alone
+// makes that part visible to it (no barrier: a wave need not wait for the
+// others' copies).
 #pragma once
 #include "kernels.h"
 #include "qcommon.h"
@@ -141,7 +145,7 @@ template <int TX, int SB, int GS, bool EPI, int TILES, int KW>
 __global__ __launch_bounds__(512) void qgemv_dec_kernel(const void* __restrict__ x, const uint32_t* __restrict__ wq,
                                                         const void* __restrict__ scales,
                                                         const void* __restrict__ biases, void* __restrict__ y,
-                                                        int M, int K, int N, Epilogue ep) {
+                                                        int M, int K, int N, int xw, Epilogue ep) {
     using F = DForm<TX>;
     using Q = DGeo<GS, SB, KW>;
     static_assert(dec_ok<GS, SB, TILES, KW>(), "block shape");
@@ -159,9 +163,13 @@ __global__ __launch_bounds__(512) void qgemv_dec_kernel(const void* __restrict__
     // ---- 1. x rows into LDS (DMA) ----
     {
         const auto xr = buf_rsrc(x, (uint32_t)M * K * 2);
-        const int kc = K / 8;  // 16-byte chunks per x row (a multiple of 64)
+        // 16-byte chunks of an x row: all K (a multiple of 64 chunks) shared by
+        // the block's waves, or the wave's own KW codes (a multiple of 64 chunks)
+        const int c_first = xw ? wave * (kKW / 8) : wave * 64;
+        const int c_end = xw ? (wave + 1) * (kKW / 8) : K / 8;
+        const int c_step = xw ? 64 : 64 * nwaves;
         for (int m = 0; m < M; m++)
-            for (int c0 = wave * 64; c0 < kc; c0 += 64 * nwaves)
+            for (int c0 = c_first; c0 < c_end; c0 += c_step)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(lds + m * XS + c0 * 16), 16,
                                                          (uint32_t)(m * K * 2 + (c0 + lane) * 16), 0, 0, 0);
     }
@@ -202,13 +210,13 @@ __global__ __launch_bounds__(512) void qgemv_dec_kernel(const void* __restrict__
     }
     __builtin_amdgcn_sched_barrier(0);
     // ---- 3. the x DMA was issued before the scale and weight loads: wait
-    // for it alone, then the barrier publishes every wave's part ----
+    // for it alone, then (xw = 0) the barrier publishes every wave's part ----
     {
         constexpr int NW = kSegs * 2 * kTiles + 2 * kTiles * Q::kSbLoads;
         static_assert(NW < 64, "vmcnt holds 6 bits");
         __builtin_amdgcn_s_waitcnt((NW & 0xF) | ((NW >> 4) << 14) | (0x7 << 4) | (0xF << 8));
     }
-    __builtin_amdgcn_s_barrier();
+    if (!xw) __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 4. segments in arrival order ----

@@ -13,6 +13,13 @@ namespace dec {
 //   K = 4096, N = 4096 (128 2-tile blocks): 2 tiles 7.4 / 7.8 / 8.0, 1 tile 5.9 / 6.2 / 6.4
 //   K = 8192, N = 8192, M = 4 / 8: 2 tiles 16.3 / 16.9, 1 tile 14.8 / 19.0
 //     (at M = 8 one 1-tile block fills a CU's LDS: the 512 blocks run in two rounds)
+// x staging: shared by the block's waves (one barrier) up to K = 4096, per
+// wave above (no barrier).  Measured, per wave against shared: K = 8192,
+// M = 8, N = 8192 14.9 us against 17.0, N = 28672 47.2 against 54.5;
+// K = 6144, N = 8192, M = 4 / 8 11.5-11.8 / 12.0 against 12.2-12.5 / 13.2;
+// at K = 4096 per wave costs 0-5 % (c1 M = 4 12.3-12.6 against 12.0-12.6;
+// N = 4096, M = 4 6.18 against 5.9).
+constexpr int kDecSharedXMaxK = 4096;
 constexpr int kCUs = 256;           // gfx950 (MI355X)
 constexpr int kWavesPerCU1 = 20;    // 1-tile kernel: <= 96 VGPRs, 5 waves per SIMD
 
@@ -29,7 +36,7 @@ LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     if (attr != hipSuccess) return LuxStatus::Internal;
     const int blocks = (a.N + 16 * TILES - 1) / (16 * TILES);
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * (a.K / KW)), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.M,
-                       a.K, a.N, a.epi());
+                       a.K, a.N, a.K > kDecSharedXMaxK ? 1 : 0, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 
