@@ -42,7 +42,7 @@ extern "C" {
 /* kernel selection for op_quantized_matmul_ex */
 typedef enum {
     LUX_QMM_KERNEL_AUTO = 0, /* GEMV for M <= threshold, else GEMM */
-    LUX_QMM_KERNEL_GEMV = 1, /* bandwidth-bound dequant-GEMV (any M, built for M <= 8) */
+    LUX_QMM_KERNEL_GEMV = 1, /* bandwidth-bound dequant-GEMV (any M, built for M <= 16) */
     LUX_QMM_KERNEL_GEMM = 2, /* MFMA GEMM (16-bit activations only) */
 } LuxQuantKernel;
 

@@ -255,15 +255,24 @@ LuxBackendError check_format(int K, int N, int group_size, int bits) {
 
 bool fits(HipBuffer* b, size_t need) { return b && (need == 0 || (b->ptr && b->size >= need)); }
 
-// M up to this value goes to the GEMV; LUX_HIP_GEMV_MAX_M overrides
-int gemv_max_m() {
-    static const int v = [] {
+// M up to this value goes to the GEMV: LUX_HIP_GEMV_MAX_M when set, else 8,
+// or 16 where the GEMV family's MFMA kernels take the shape (16-bit x, 4- or
+// 8-bit codes, K % 1024 == 0).  There they measured faster than the small-M
+// GEMM (graph replays): 4-bit K = 4096, N = 14336, M = 9 / 12 / 16 15.2 /
+// 15.7 / 16.3 us against 21.0-21.2, N = 28672, M = 16 29.3 against 39.8;
+// 8-bit K = 4096, N = 14336, M = 12 / 16 23.7 against 26.0 / 26.3, K = N =
+// 8192 20.9 / 21.3 against 22.8 / 23.2.  3- and 6-bit codes at M = 16 run
+// 2.2x slower on the GEMV side, so their crossover stays at 8.
+int gemv_max_m(int K, int bits, LuxBackendDtype x_dtype) {
+    static const int env = [] {
         const char* e = std::getenv("LUX_HIP_GEMV_MAX_M");
-        int d = 8;
-        if (e && *e) d = std::atoi(e);
+        if (!e || !*e) return -1;
+        const int d = std::atoi(e);
         return d < 0 ? 0 : d;
     }();
-    return v;
+    if (env >= 0) return env;
+    const bool mfma_gemv = x_dtype != LUX_DTYPE_FLOAT32 && (bits == 4 || bits == 8) && K % 1024 == 0;
+    return mfma_gemv ? 16 : 8;
 }
 
 // shapes the MFMA GEMMs take: 16-bit activations, and
@@ -285,7 +294,7 @@ bool gemm_ok(int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dt
 
 LuxQuantKernel select_kernel_impl(int M, int K, int N, int group_size, int bits,
                                   LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype) {
-    if (M <= gemv_max_m() || !gemm_ok(M, K, N, group_size, bits, x_dtype, sb_dtype))
+    if (M <= gemv_max_m(K, bits, x_dtype) || !gemm_ok(M, K, N, group_size, bits, x_dtype, sb_dtype))
         return LUX_QMM_KERNEL_GEMV;
     return LUX_QMM_KERNEL_GEMM;
 }

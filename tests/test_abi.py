@@ -118,6 +118,16 @@ def test_quant_extension_table_without_gpu():
     assert q.select_kernel(2048, 4160, 4096, 64, 4, abi.BFLOAT16, abi.BFLOAT16) == abi.KERNEL_GEMV
     assert q.select_kernel(2048, 4096, 4096, 32, 8, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMV
     assert q.select_kernel(2048, 4096, 4096, 32, 4, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMM
+    # the GEMV/GEMM crossover: M = 16 for 4/8-bit codes with K % 1024 == 0
+    # and 16-bit x (the GEMV's MFMA kernels), else M = 8
+    if not os.environ.get("LUX_HIP_GEMV_MAX_M"):
+        for bits in (4, 8):
+            assert q.select_kernel(16, 4096, 14336, 64, bits, abi.FLOAT16, abi.FLOAT16) == abi.KERNEL_GEMV
+            assert q.select_kernel(17, 4096, 14336, 64, bits, abi.FLOAT16, abi.FLOAT16) == abi.KERNEL_GEMM
+        for bits in (3, 6):
+            assert q.select_kernel(8, 4096, 11008, 64, bits, abi.FLOAT16, abi.FLOAT16) == abi.KERNEL_GEMV
+            assert q.select_kernel(9, 4096, 11008, 64, bits, abi.FLOAT16, abi.FLOAT16) == abi.KERNEL_GEMM
+        assert q.select_kernel(12, 3328, 4096, 64, 4, abi.BFLOAT16, abi.BFLOAT16) == abi.KERNEL_GEMM
     # NULL context / buffers are rejected before any device work
     assert q.op_quantized_matmul(None, None, None, None, None, None, 1, 64, 1, 64, 4, 1, 1, 1) == \
         abi.ERR_INVALID_ARGUMENT
