@@ -39,7 +39,9 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     }
     int chunk = 8;
     while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
-    if (gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) return LuxStatus::NotSupported;
+    // one row of x may still run on the split-K stream kernel (K <= 32768),
+    // which stages x in up to 160 KB; the row-run kernel declines it itself
+    if (args.M > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) return LuxStatus::NotSupported;
     for (int m0 = 0; m0 < args.M; m0 += chunk) {
         QmmArgs a = args;
         a.M = args.M - m0 < chunk ? args.M - m0 : chunk;

@@ -654,6 +654,220 @@ LuxStatus launch_stream_r(const QmmArgs& a, hipStream_t st) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K streaming kernel: M == 1, 4096 < K <= 32768.
+//
+// The stream kernel's arithmetic with K split over the waves of a block: a
+// block owns R rows; its KS = ceil(K / 4096) waves split K into parts of
+// PU <= 64 units (one 64-code unit per lane), each wave loads its part of the
+// R rows straight into registers and computes the R partials as the stream
+// kernel does, and the parts meet in LDS.  x (all of K, units swizzled as in
+// the stream kernel) and the block's R scale and bias rows are copied into
+// (dynamic) LDS by buffer->LDS DMA once per block; one vmcnt wait plus a
+// barrier publishes them while the weight loads stay in flight.
+// ---------------------------------------------------------------------------
+constexpr int kSplitMaxWaves = 8;
+constexpr int kSplitRows = 4;
+
+// LDS bytes of the split kernel: x, a zero unit (read by idle lanes), then
+// scale and bias rows (16-byte aligned, with room for the lead of the first
+// row within its chunk), then the waves' partials
+__host__ __device__ constexpr size_t split_sb_bytes(int K, int gs, int sb_bytes) {
+    return ((size_t)kSplitRows * (K / gs) * sb_bytes + 16 + 15) & ~(size_t)15;
+}
+__host__ __device__ constexpr size_t split_lds_bytes(int K, int xe, int gs, int sb_bytes) {
+    return (size_t)(K + 64) * xe + 2 * split_sb_bytes(K, gs, sb_bytes) + (size_t)kSplitMaxWaves * 8 * 4;
+}
+
+template <int BITS, int TX, int SB, bool TWO, bool EPI>
+__global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
+    const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, void* __restrict__ y, int K, int N, int gshift, int pu, Epilogue ep) {
+    constexpr int R = kSplitRows;
+    // f16 x with 4-bit codes: the magic-number form, not the subnormal one.
+    // Against the oracle's fp64 accumulation the subnormal form's error
+    // grows with K (median 2.5e-6 of max|y| at K = 4096, 1e-5 at K = 14336,
+    // above the fp32 gate); the other forms stay within 2.4e-6 there.
+    constexpr int OP = op_kind<BITS, TX>() == OP_SUB4 ? OP_MAGIC : op_kind<BITS, TX>();
+    constexpr int XE = TX == DT_F32 ? 4 : 2;
+    constexpr int W = 2 * BITS;
+    constexpr int kSb = SB == DT_F32 ? 4 : 2;
+    static_assert(R <= 8, "one sum8 pass");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int units = K >> 6;
+    const int u = wave * pu + lane;                 // this lane's unit
+    const bool active = lane < pu && u < units;
+    const int G = K >> gshift;
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+    const uint32_t sb_row = (uint32_t)G * kSb;
+    const int n0 = blockIdx.x * R;
+    const size_t sbb = split_sb_bytes(K, 1 << gshift, kSb);
+    uint8_t* const lx = lds;
+    uint8_t* const lzero = lds + (size_t)K * XE;  // one unit of zeros
+    uint8_t* const lsd = lzero + 64 * XE;
+    uint8_t* const lbd = lsd + sbb;
+    float* const red = reinterpret_cast<float*>(lbd + sbb);
+
+    // scale rows of the block from the 16-byte chunk holding row n0's first
+    const size_t sb_first = (size_t)n0 * sb_row;
+    const uint32_t sb_lead = (uint32_t)(sb_first & 15u);
+    const size_t sb_base = sb_first - sb_lead;
+
+    // ---- 1. x and the block's scale/bias rows into LDS, and the zero unit ----
+    {
+        if (wave == 0 && lane < 4 * XE) *reinterpret_cast<v4u32*>(lzero + lane * 16) = v4u32{0u, 0u, 0u, 0u};
+        const auto xr = buf_rsrc(x, (uint32_t)K * XE);
+        constexpr int CPU = 4 * XE;  // 16-byte chunks per 64-element unit
+        const int kc = K * XE / 16;
+        for (int cw = wave * 64; cw < kc; cw += 64 * nwaves) {
+            const int cc = cw + lane;
+            if (cc < kc) {
+                // LDS slot cc holds the unit's chunk (cc % CPU) ^ swz, read back by prep_x
+                const int xu = cc / CPU, src = xu * CPU + ((cc % CPU) ^ x_swz<XE>(xu));
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(lx + cw * 16), 16, (uint32_t)src * 16, 0, 0, 0);
+            }
+        }
+        const size_t sleft = (((size_t)N * sb_row - sb_base) + 15u) & ~(size_t)15u;
+        const uint32_t sbytes = (uint32_t)(sleft < 0x7fffffffu ? sleft : 0x7fffffffu);
+        const auto sr = buf_rsrc(static_cast<const uint8_t*>(scales) + sb_base, sbytes);
+        const auto br = buf_rsrc(static_cast<const uint8_t*>(biases) + sb_base, sbytes);
+        // all R rows: chunks past the array read zeros (rows past N)
+        const int sc = (int)((sb_lead + (uint32_t)R * sb_row + 15) / 16);
+        for (int cw = wave * 64; cw < sc; cw += 64 * nwaves) {
+            if (cw + lane < sc) {
+                const uint32_t voff = (uint32_t)(cw + lane) * 16;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_ptr)(lsd + cw * 16), 16, voff, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_ptr)(lbd + cw * 16), 16, voff, 0, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. this wave's part of the block's rows into registers; rows past
+    // N re-read row N-1 (never stored), idle lanes read zeros ----
+    uint32_t w[R][W];
+    {
+        const size_t wleft = (size_t)(N - n0) * row_bytes;
+        const auto wr = buf_rsrc(reinterpret_cast<const uint8_t*>(wq) + (size_t)n0 * row_bytes,
+                                 (uint32_t)(wleft < 0x7fffffffu ? wleft : 0x7fffffffu));
+        const uint32_t voff = active ? (uint32_t)u * (8 * BITS) : kZeroOff;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int n = n0 + r < N ? n0 + r : N - 1;
+            load_unit_buf<BITS>(wr, voff, (uint32_t)(n - n0) * row_bytes, w[r]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- 3. this wave's DMAs were issued before its NW weight loads: wait
+    // for them (and for the zero unit's LDS writes), then the barrier
+    // publishes every wave's part.  The count holds only while every weight
+    // load is issued above: every lane uses every row's words below, with no
+    // lane-dependent branch the compiler could sink a row's loads into. ----
+    {
+        constexpr int NW = R * unit_loads<BITS>();
+        static_assert(NW < 64, "vmcnt holds 6 bits");
+        __builtin_amdgcn_s_waitcnt((NW & 0xF) | ((NW >> 4) << 14) | (0x7 << 4));
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 4. x operands of the lane's unit (idle lanes: the zero unit, zero
+    // codes and zero scales, so their partials are exactly 0), then the rows
+    // in arrival order ----
+    XOps<BITS, TX, OP> xo;
+    prep_x<BITS, TX, OP>(active ? lx + (size_t)u * 64 * XE : lzero, active ? x_swz<XE>(u) : 0, xo);
+    const int uc = active ? u : 0;
+    const int g0 = (uc << 6) >> gshift;
+    const uint8_t* ls = lsd + sb_lead + g0 * kSb;
+    const uint8_t* lb = lbd + sb_lead + g0 * kSb;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float s0, b0, s1 = 0.f, b1 = 0.f;
+        if constexpr (SB == DT_F32) {
+            const float* ps = reinterpret_cast<const float*>(ls + r * sb_row);
+            const float* pb = reinterpret_cast<const float*>(lb + r * sb_row);
+            s0 = ps[0];
+            b0 = pb[0];
+            if constexpr (TWO) { s1 = ps[1]; b1 = pb[1]; }
+        } else {
+            const uint16_t* ps = reinterpret_cast<const uint16_t*>(ls + r * sb_row);
+            const uint16_t* pb = reinterpret_cast<const uint16_t*>(lb + r * sb_row);
+            s0 = SB == DT_F16 ? f16_to_f32(ps[0]) : bf16_to_f32(ps[0]);
+            b0 = SB == DT_F16 ? f16_to_f32(pb[0]) : bf16_to_f32(pb[0]);
+            if constexpr (TWO) {
+                s1 = SB == DT_F16 ? f16_to_f32(ps[1]) : bf16_to_f32(ps[1]);
+                b1 = SB == DT_F16 ? f16_to_f32(pb[1]) : bf16_to_f32(pb[1]);
+            }
+        }
+        if (!active) s0 = b0 = s1 = b1 = 0.f;
+        acc[r] = row_partial<BITS, TX, OP, TWO>(w[r], xo, s0, b0, s1, b1);
+    }
+
+    // ---- 5. lane sums (lanes with (lane & 7) == 0 hold value sum8_index),
+    // then the K parts meet in LDS and wave 0 stores ----
+    const float z = sum8(acc, lane) * out_scale<OP>();
+    if ((lane & 7) == 0) red[wave * 8 + sum8_index(lane)] = z;
+    __syncthreads();
+    if (wave == 0 && lane < R) {
+        float t = 0.f;
+        for (int p = 0; p < nwaves; p++) t += red[p * 8 + lane];
+        const int n = n0 + lane;
+        if (n < N) store_out<EPI>(y, (size_t)n, n, ep, t);
+    }
+}
+
+template <int BITS, int TX, int SB, bool TWO, bool EPI>
+LuxStatus launch_split_k(const QmmArgs& a, hipStream_t st, int ks, int pu, size_t lds) {
+    auto kern = qgemv_split_kernel<BITS, TX, SB, TWO, EPI>;
+    // once per instantiation; a function-local static initializes exactly once
+    // even when several threads make the first call together
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return LuxStatus::Internal;
+    const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
+    const int blocks = (a.N + kSplitRows - 1) / kSplitRows;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * ks), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.K, a.N,
+                       gshift, pu, a.epi());
+    return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+// M == 1, 4096 < K <= 32768 (K % 64 == 0), x, scales and rows of 32-bit
+// offsets, LDS within 160 KB; NotSupported otherwise
+template <int BITS, int TX, int SB>
+LuxStatus launch_split_sb(const QmmArgs& a, hipStream_t st) {
+    if (a.M != 1 || a.K <= 4096 || a.K % 64 != 0) return LuxStatus::NotSupported;
+    const int units = a.K / 64;
+    const int ks = (units + 63) / 64;
+    if (ks > kSplitMaxWaves) return LuxStatus::NotSupported;
+    const int pu = (units + ks - 1) / ks;
+    constexpr int XE = TX == DT_F32 ? 4 : 2, kSb = SB == DT_F32 ? 4 : 2;
+    const size_t lds = split_lds_bytes(a.K, XE, a.group_size, kSb);
+    if (lds > 160 * 1024) return LuxStatus::NotSupported;
+    // one block's scale rows and its weight rows (relative to the block's
+    // first row) stay far below 2^31; x is below 128 KB
+    const bool epi = a.has_epilogue();
+    if (a.group_size == 32)
+        return epi ? launch_split_k<BITS, TX, SB, true, true>(a, st, ks, pu, lds)
+                   : launch_split_k<BITS, TX, SB, true, false>(a, st, ks, pu, lds);
+    return epi ? launch_split_k<BITS, TX, SB, false, true>(a, st, ks, pu, lds)
+               : launch_split_k<BITS, TX, SB, false, false>(a, st, ks, pu, lds);
+}
+
+template <int BITS, int TX>
+LuxStatus launch_split(const QmmArgs& a, hipStream_t st) {
+    switch (a.sb_dtype) {
+    case DT_F32: return launch_split_sb<BITS, TX, DT_F32>(a, st);
+    case DT_F16: return launch_split_sb<BITS, TX, DT_F16>(a, st);
+    default: return launch_split_sb<BITS, TX, DT_BF16>(a, st);
+    }
+}
+
 template <int BITS, int TX, int MR, bool EPI>
 LuxStatus launch_t_e(const QmmArgs& a, hipStream_t st) {
     constexpr int RU = 4;
@@ -687,6 +901,10 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
 
 template <int BITS, int TX>
 LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
+    if (a.M == 1 && a.K > 4096) {
+        const LuxStatus s = launch_split<BITS, TX>(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     if (a.K <= 4096 && (a.M <= 4 && (TX != DT_F32 || a.M == 1))) {
         if (a.M <= 1) return launch_stream_r<BITS, TX, 1>(a, st);
         if constexpr (TX != DT_F32) {

@@ -104,6 +104,41 @@ def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"gemv b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F32, F32, F32),
+                                       (F16, F32, F32), (BF16, F16, F32)])
+def test_split_k_gemv_parity(ctx, oracle, bits, xd, sbd, od):
+    """M = 1 with 4096 < K <= 32768 runs the split-K stream kernel: parts of
+    64 units (K = 8192: 2 waves), uneven parts with idle lanes (K = 5120:
+    2 x 40 units; K = 14336: 4 x 56), 7 and 8 waves (K = 28672, 32768; f32
+    x at K = 32768 exceeds its LDS and runs the generic kernel), every group
+    size, N not a multiple of the 4-row block.  fp32 outputs with K > 8192
+    meet the fp32 gate (1e-5 of max|y|) against the oracle's fp64
+    accumulation: over that many terms the sequential fp32 oracle's own
+    rounding reaches ~1e-5 (measured 1.3e-5 between it and this kernel at
+    K = 14336)."""
+    O = oracle
+    for (K, N, gs) in [(5120, 37, 128), (8192, 50, 32), (14336, 21, 64), (28672, 13, 64), (32768, 9, 32)]:
+        x, w_q, s, b, _ = O.make_problem(1, K, N, bits, gs, xd, sbd, seed=bits * 17 + K)
+        y = run(ctx, x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
+        if od == F32 and K > 8192:
+            want = O.quantized_matmul(x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od, variant="f64").astype(np.float32)
+        else:
+            want = O.quantized_matmul(x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"split-K b{bits} K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("K,N,xd", [(14336, 4096, F16), (28672, 8192, BF16)])
+def test_split_k_full(ctx, oracle, K, N, xd):
+    """Model-sized M = 1 shapes on the split-K kernel: a down projection
+    (K = 14336, N = 4096) and K = 28672, N = 8192; 4-bit g64."""
+    O = oracle
+    x, w_q, s, b, _ = O.make_problem(1, K, N, 4, 64, xd, xd, seed=K + N)
+    y = run(ctx, x, w_q, s, b, 1, K, N, 64, 4, xd, xd, xd)
+    want = O.quantized_matmul(x, w_q, s, b, 1, K, N, 64, 4, xd, xd, xd, variant="omp")
+    check_output(O, y, want, xd, f"split-K full K{K} N{N}")
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
