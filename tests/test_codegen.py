@@ -1,0 +1,82 @@
+"""Wait counts of the stream, split-K and decode GEMV kernels, checked in the
+built gfx950 code (llvm-objdump of the plugin's own code objects).
+
+Each of these kernels copies x (and scales) into LDS by buffer->LDS DMA,
+then issues its weight loads into registers, then waits with
+`s_waitcnt vmcnt(n)` for n = the number of those weight loads and crosses
+a barrier: the wait means "every DMA before them has landed" only if all n
+register loads are issued before it.  The compiler may still move a load
+into a later, lane-conditional block (it did once, for a per-lane select of
+the partial sums), and then the wait silently stops covering the DMA.  This
+test counts, per kernel, the register-returning buffer loads issued before
+the first `s_barrier` and checks them against the wait's count.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+LLVM = "/opt/rocm/llvm/bin"
+KERNELS = ("qgemv_stream_kernel", "qgemv_split_kernel", "qgemv_dec_kernel")
+
+
+def _tool(name):
+    p = os.path.join(LLVM, name)
+    return p if os.path.exists(p) else shutil.which(name)
+
+
+@pytest.fixture(scope="module")
+def disassembly(tmp_path_factory):
+    import mlx_amd
+    objdump = _tool("llvm-objdump")
+    if not objdump:
+        pytest.skip("llvm-objdump not available")
+    assert os.path.exists(mlx_amd.PLUGIN_PATH), "run __graft_entry__.build() first"
+    d = tmp_path_factory.mktemp("codeobj")
+    so = d / "plugin.so"
+    shutil.copy(mlx_amd.PLUGIN_PATH, so)
+    # --offloading writes the embedded device code objects next to its input
+    subprocess.run([objdump, "--offloading", str(so)], cwd=d, check=True, capture_output=True)
+    out = {}
+    for co in sorted(d.glob("plugin.so.*gfx950*")):
+        syms = subprocess.run([objdump, "-t", str(co)], check=True, capture_output=True, text=True).stdout
+        names = [ln.split()[-1] for ln in syms.splitlines()
+                 if " .text" in ln and any(k in ln for k in KERNELS) and not ln.endswith(".kd")]
+        if not names:
+            continue
+        dis = subprocess.run([objdump, "-d", "--mcpu=gfx950", "--disassemble-symbols=" + ",".join(names), str(co)],
+                             check=True, capture_output=True, text=True).stdout
+        cur = None
+        for ln in dis.splitlines():
+            m = re.match(r"^[0-9a-f]+ <(\S+)>:", ln)
+            if m:
+                cur = m.group(1)
+                out[cur] = []
+            elif cur and ln.strip():
+                out[cur].append(ln.strip())
+    return out
+
+
+def test_weight_loads_precede_their_wait(disassembly):
+    found = {k: 0 for k in KERNELS}
+    bad = []
+    for name, lines in disassembly.items():
+        loads, vm = 0, None
+        for t in lines:
+            if t.startswith("buffer_load") and not re.search(r"\blds\b", t):
+                loads += 1
+            m = re.search(r"s_waitcnt\b.*\bvmcnt\((\d+)\)", t)
+            if m:
+                vm = int(m.group(1))
+            if t.startswith("s_barrier"):
+                break
+        else:
+            continue  # no barrier: nothing to check
+        for k in KERNELS:
+            found[k] += k in name
+        if vm is not None and loads < vm:
+            bad.append(f"{name}: {loads} loads before vmcnt({vm})")
+    assert all(found.values()), f"kernels not found in the plugin: {found}"
+    assert not bad, "\n".join(bad[:10])
