@@ -23,7 +23,11 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     //    6 / 8 at K = 4096, N = 14336: 18.1 / 19.5 / 19.9 / 20.1 us against
     //    22.7 / 22.9 / 23.1 / 23.2; M = 4, N = 4096: 7.2 against 10.5 (at
     //    K = 8192 the LDS-ring kernel stays: 20.2 against 25.0).
-    const bool stream2 = args.M == 2 && args.K <= 4096 && args.x_dtype != DT_F32;
+    //  - M = 2, 16-bit x, 8192 < K <= 16384: the split-K stream kernel
+    //    (K = 14336, N = 4096: 18.1 us against 25.7 on the LDS-ring kernel;
+    //    8-bit K = 12288: 17.7 against 25.3); at K <= 8192 the decode kernel
+    //    is faster (K = 8192, N = 8192: 12.8 against 18.1).
+    const bool stream2 = args.M == 2 && args.x_dtype != DT_F32 && (args.K <= 4096 || (args.K > 8192 && args.K <= 16384));
     const bool ring8 = !(args.bits == 8 && args.M <= 8 && args.K <= 4096);
     if (args.M >= 2 && args.M <= 8 && !stream2) {
         const LuxStatus s = launch_qgemv_dec(args, st);

@@ -655,13 +655,13 @@ LuxStatus launch_stream_r(const QmmArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K streaming kernel: M == 1, 4096 < K <= 32768.
+// Split-K streaming kernel: M == MR (1, or 2 with 16-bit x), 4096 < K <= 32768.
 //
 // The stream kernel's arithmetic with K split over the waves of a block: a
 // block owns R rows; its KS = ceil(K / 4096) waves split K into parts of
 // PU <= 64 units (one 64-code unit per lane), each wave loads its part of the
-// R rows straight into registers and computes the R partials as the stream
-// kernel does, and the parts meet in LDS.  x (all of K, units swizzled as in
+// R rows straight into registers and computes the R x MR partials as the
+// stream kernel does, and the parts meet in LDS.  x (MR rows, all of K, units swizzled as in
 // the stream kernel) and the block's R scale and bias rows are copied into
 // (dynamic) LDS by buffer->LDS DMA once per block; one vmcnt wait plus a
 // barrier publishes them while the weight loads stay in flight.
@@ -675,11 +675,11 @@ constexpr int kSplitRows = 4;
 __host__ __device__ constexpr size_t split_sb_bytes(int K, int gs, int sb_bytes) {
     return ((size_t)kSplitRows * (K / gs) * sb_bytes + 16 + 15) & ~(size_t)15;
 }
-__host__ __device__ constexpr size_t split_lds_bytes(int K, int xe, int gs, int sb_bytes) {
-    return (size_t)(K + 64) * xe + 2 * split_sb_bytes(K, gs, sb_bytes) + (size_t)kSplitMaxWaves * 8 * 4;
+__host__ __device__ constexpr size_t split_lds_bytes(int mr, int K, int xe, int gs, int sb_bytes) {
+    return ((size_t)mr * K + 64) * xe + 2 * split_sb_bytes(K, gs, sb_bytes) + (size_t)kSplitMaxWaves * 8 * 4;
 }
 
-template <int BITS, int TX, int SB, bool TWO, bool EPI>
+template <int BITS, int TX, int SB, int MR, bool TWO, bool EPI>
 __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int K, int N, int gshift, int pu, Epilogue ep) {
@@ -692,7 +692,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     constexpr int XE = TX == DT_F32 ? 4 : 2;
     constexpr int W = 2 * BITS;
     constexpr int kSb = SB == DT_F32 ? 4 : 2;
-    static_assert(R <= 8, "one sum8 pass");
+    static_assert(R * MR <= 8, "one sum8 pass");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     const int n0 = blockIdx.x * R;
     const size_t sbb = split_sb_bytes(K, 1 << gshift, kSb);
     uint8_t* const lx = lds;
-    uint8_t* const lzero = lds + (size_t)K * XE;  // one unit of zeros
+    uint8_t* const lzero = lds + (size_t)MR * K * XE;  // one unit of zeros
     uint8_t* const lsd = lzero + 64 * XE;
     uint8_t* const lbd = lsd + sbb;
     float* const red = reinterpret_cast<float*>(lbd + sbb);
@@ -719,14 +719,15 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     // ---- 1. x and the block's scale/bias rows into LDS, and the zero unit ----
     {
         if (wave == 0 && lane < 4 * XE) *reinterpret_cast<v4u32*>(lzero + lane * 16) = v4u32{0u, 0u, 0u, 0u};
-        const auto xr = buf_rsrc(x, (uint32_t)K * XE);
+        const auto xr = buf_rsrc(x, (uint32_t)MR * K * XE);
         constexpr int CPU = 4 * XE;  // 16-byte chunks per 64-element unit
-        const int kc = K * XE / 16;
-        for (int cw = wave * 64; cw < kc; cw += 64 * nwaves) {
+        const int kc = K * XE / 16;  // chunks of one x row
+        for (int cw = wave * 64; cw < MR * kc; cw += 64 * nwaves) {
             const int cc = cw + lane;
-            if (cc < kc) {
-                // LDS slot cc holds the unit's chunk (cc % CPU) ^ swz, read back by prep_x
-                const int xu = cc / CPU, src = xu * CPU + ((cc % CPU) ^ x_swz<XE>(xu));
+            if (cc < MR * kc) {
+                // LDS slot c of row m holds the unit's chunk (c % CPU) ^ swz, read back by prep_x
+                const int m = cc / kc, c = cc % kc;
+                const int xu = c / CPU, src = m * kc + xu * CPU + ((c % CPU) ^ x_swz<XE>(xu));
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(lx + cw * 16), 16, (uint32_t)src * 16, 0, 0, 0);
             }
         }
@@ -777,8 +778,11 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     // ---- 4. x operands of the lane's unit (idle lanes: the zero unit, zero
     // codes and zero scales, so their partials are exactly 0), then the rows
     // in arrival order ----
-    XOps<BITS, TX, OP> xo;
-    prep_x<BITS, TX, OP>(active ? lx + (size_t)u * 64 * XE : lzero, active ? x_swz<XE>(u) : 0, xo);
+    XOps<BITS, TX, OP> xo[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+        prep_x<BITS, TX, OP>(active ? lx + ((size_t)m * K + (size_t)u * 64) * XE : lzero, active ? x_swz<XE>(u) : 0,
+                             xo[m]);
     const int uc = active ? u : 0;
     const int g0 = (uc << 6) >> gshift;
     const uint8_t* ls = lsd + sb_lead + g0 * kSb;
@@ -806,7 +810,8 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
             }
         }
         if (!active) s0 = b0 = s1 = b1 = 0.f;
-        acc[r] = row_partial<BITS, TX, OP, TWO>(w[r], xo, s0, b0, s1, b1);
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r * MR + m] = row_partial<BITS, TX, OP, TWO>(w[r], xo[m], s0, b0, s1, b1);
     }
 
     // ---- 5. lane sums (lanes with (lane & 7) == 0 hold value sum8_index),
@@ -814,17 +819,17 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     const float z = sum8(acc, lane) * out_scale<OP>();
     if ((lane & 7) == 0) red[wave * 8 + sum8_index(lane)] = z;
     __syncthreads();
-    if (wave == 0 && lane < R) {
+    if (wave == 0 && lane < R * MR) {
         float t = 0.f;
         for (int p = 0; p < nwaves; p++) t += red[p * 8 + lane];
-        const int n = n0 + lane;
-        if (n < N) store_out<EPI>(y, (size_t)n, n, ep, t);
+        const int n = n0 + lane / MR, m = lane % MR;
+        if (n < N) store_out<EPI>(y, (size_t)m * N + n, n, ep, t);
     }
 }
 
-template <int BITS, int TX, int SB, bool TWO, bool EPI>
+template <int BITS, int TX, int SB, int MR, bool TWO, bool EPI>
 LuxStatus launch_split_k(const QmmArgs& a, hipStream_t st, int ks, int pu, size_t lds) {
-    auto kern = qgemv_split_kernel<BITS, TX, SB, TWO, EPI>;
+    auto kern = qgemv_split_kernel<BITS, TX, SB, MR, TWO, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -837,34 +842,34 @@ LuxStatus launch_split_k(const QmmArgs& a, hipStream_t st, int ks, int pu, size_
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 
-// M == 1, 4096 < K <= 32768 (K % 64 == 0), x, scales and rows of 32-bit
-// offsets, LDS within 160 KB; NotSupported otherwise
-template <int BITS, int TX, int SB>
+// M == MR rows of x, 4096 < K <= 32768 (K % 64 == 0), x, scales and rows
+// of 32-bit offsets, LDS within 160 KB; NotSupported otherwise
+template <int BITS, int TX, int SB, int MR>
 LuxStatus launch_split_sb(const QmmArgs& a, hipStream_t st) {
-    if (a.M != 1 || a.K <= 4096 || a.K % 64 != 0) return LuxStatus::NotSupported;
+    if (a.M != MR || a.K <= 4096 || a.K % 64 != 0) return LuxStatus::NotSupported;
     const int units = a.K / 64;
     const int ks = (units + 63) / 64;
     if (ks > kSplitMaxWaves) return LuxStatus::NotSupported;
     const int pu = (units + ks - 1) / ks;
     constexpr int XE = TX == DT_F32 ? 4 : 2, kSb = SB == DT_F32 ? 4 : 2;
-    const size_t lds = split_lds_bytes(a.K, XE, a.group_size, kSb);
+    const size_t lds = split_lds_bytes(MR, a.K, XE, a.group_size, kSb);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
     // one block's scale rows and its weight rows (relative to the block's
     // first row) stay far below 2^31; x is below 128 KB
     const bool epi = a.has_epilogue();
     if (a.group_size == 32)
-        return epi ? launch_split_k<BITS, TX, SB, true, true>(a, st, ks, pu, lds)
-                   : launch_split_k<BITS, TX, SB, true, false>(a, st, ks, pu, lds);
-    return epi ? launch_split_k<BITS, TX, SB, false, true>(a, st, ks, pu, lds)
-               : launch_split_k<BITS, TX, SB, false, false>(a, st, ks, pu, lds);
+        return epi ? launch_split_k<BITS, TX, SB, MR, true, true>(a, st, ks, pu, lds)
+                   : launch_split_k<BITS, TX, SB, MR, true, false>(a, st, ks, pu, lds);
+    return epi ? launch_split_k<BITS, TX, SB, MR, false, true>(a, st, ks, pu, lds)
+               : launch_split_k<BITS, TX, SB, MR, false, false>(a, st, ks, pu, lds);
 }
 
-template <int BITS, int TX>
+template <int BITS, int TX, int MR>
 LuxStatus launch_split(const QmmArgs& a, hipStream_t st) {
     switch (a.sb_dtype) {
-    case DT_F32: return launch_split_sb<BITS, TX, DT_F32>(a, st);
-    case DT_F16: return launch_split_sb<BITS, TX, DT_F16>(a, st);
-    default: return launch_split_sb<BITS, TX, DT_BF16>(a, st);
+    case DT_F32: return launch_split_sb<BITS, TX, DT_F32, MR>(a, st);
+    case DT_F16: return launch_split_sb<BITS, TX, DT_F16, MR>(a, st);
+    default: return launch_split_sb<BITS, TX, DT_BF16, MR>(a, st);
     }
 }
 
@@ -902,8 +907,14 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
 template <int BITS, int TX>
 LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
     if (a.M == 1 && a.K > 4096) {
-        const LuxStatus s = launch_split<BITS, TX>(a, st);
+        const LuxStatus s = launch_split<BITS, TX, 1>(a, st);
         if (s != LuxStatus::NotSupported) return s;
+    }
+    if constexpr (TX != DT_F32) {
+        if (a.M == 2 && a.K > 4096) {
+            const LuxStatus s = launch_split<BITS, TX, 2>(a, st);
+            if (s != LuxStatus::NotSupported) return s;
+        }
     }
     if (a.K <= 4096 && (a.M <= 4 && (TX != DT_F32 || a.M == 1))) {
         if (a.M <= 1) return launch_stream_r<BITS, TX, 1>(a, st);

@@ -108,7 +108,8 @@ def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F32, F32, F32),
                                        (F16, F32, F32), (BF16, F16, F32)])
 def test_split_k_gemv_parity(ctx, oracle, bits, xd, sbd, od):
-    """M = 1 with 4096 < K <= 32768 runs the split-K stream kernel: parts of
+    """M = 1 with 4096 < K <= 32768 (and M = 2 with 16-bit x and
+    8192 < K <= 16384) runs the split-K stream kernel: parts of
     64 units (K = 8192: 2 waves), uneven parts with idle lanes (K = 5120:
     2 x 40 units; K = 14336: 4 x 56), 7 and 8 waves (K = 28672, 32768; f32
     x at K = 32768 exceeds its LDS and runs the generic kernel), every group
@@ -118,14 +119,15 @@ def test_split_k_gemv_parity(ctx, oracle, bits, xd, sbd, od):
     rounding reaches ~1e-5 (measured 1.3e-5 between it and this kernel at
     K = 14336)."""
     O = oracle
-    for (K, N, gs) in [(5120, 37, 128), (8192, 50, 32), (14336, 21, 64), (28672, 13, 64), (32768, 9, 32)]:
-        x, w_q, s, b, _ = O.make_problem(1, K, N, bits, gs, xd, sbd, seed=bits * 17 + K)
-        y = run(ctx, x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
+    for (M, K, N, gs) in [(1, 5120, 37, 128), (1, 8192, 50, 32), (1, 14336, 21, 64), (1, 28672, 13, 64),
+                          (1, 32768, 9, 32), (2, 14336, 21, 64), (2, 9216, 13, 128), (2, 16384, 6, 32)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 17 + K + M)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
         if od == F32 and K > 8192:
-            want = O.quantized_matmul(x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od, variant="f64").astype(np.float32)
+            want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, variant="f64").astype(np.float32)
         else:
-            want = O.quantized_matmul(x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od)
-        check_output(O, y, want, od, f"split-K b{bits} K{K} N{N} g{gs}")
+            want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"split-K b{bits} M{M} K{K} N{N} g{gs}")
 
 
 @pytest.mark.parametrize("K,N,xd", [(14336, 4096, F16), (28672, 8192, BF16)])
