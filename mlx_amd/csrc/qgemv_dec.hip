@@ -21,11 +21,14 @@ namespace dec {
 // N = 4096, M = 4 6.18 against 5.9).
 constexpr int kDecSharedXMaxK = 4096;
 constexpr int kCUs = 256;           // gfx950 (MI355X)
+// 1-tile blocks with 512 codes per wave (K <= 4096), against 1024: K = 4096,
+// N = 4096, M = 4 / 8 5.84 / 6.12 us against 6.13 / 6.41; N = 6144, M = 4
+// 7.50 against 7.83; K = 2048, N = 8192, M = 8 5.64 against 7.12
+constexpr bool kDec1KW512 = true;
 constexpr int kWavesPerCU1 = 20;    // 1-tile kernel: <= 96 VGPRs, 5 waves per SIMD
 
-template <int TX, int SB, int GS, bool EPI, int TILES>
+template <int TX, int SB, int GS, bool EPI, int TILES, int KW = 1024>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
-    constexpr int KW = 1024;
     const size_t lds = dec_lds_bytes(a.M, a.K, TILES, KW);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
     auto kern = qgemv_dec_kernel<TX, SB, GS, EPI, TILES, KW>;
@@ -43,12 +46,21 @@ LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
 template <int TX, int SB, int GS, bool EPI>
 LuxStatus launch_kw(const QmmArgs& a, hipStream_t st) {
     static_assert(dec_ok<GS, SB, 1, 1024>() && dec_ok<GS, SB, 2, 1024>(), "block shapes");
+    // 1-tile blocks: 512 codes per wave where that keeps a block within 8 waves
+    constexpr bool kw512_ok = kDec1KW512 && dec_ok<GS, SB, 1, 512>();
+    const bool kw512 = kw512_ok && a.K / 512 <= 8;
+    const int kw1 = kw512 ? 512 : 1024;
     const long b2 = (a.N + 31) / 32, b1 = (a.N + 15) / 16;
-    const size_t lds1 = dec_lds_bytes(a.M, a.K, 1, 1024);
+    const size_t lds1 = dec_lds_bytes(a.M, a.K, 1, kw1);
     const long lds_fit = lds1 <= 160 * 1024 ? (long)(160 * 1024 / lds1) : 0;
-    const long wave_fit = kWavesPerCU1 / (a.K / 1024);
+    const long wave_fit = kWavesPerCU1 / (a.K / kw1);
     const long per_cu = lds_fit < wave_fit ? lds_fit : wave_fit;
-    if (b2 <= kCUs && b1 <= per_cu * kCUs) return launch_e<TX, SB, GS, EPI, 1>(a, st);
+    if (b2 <= kCUs && b1 <= per_cu * kCUs) {
+        if constexpr (kw512_ok) {
+            if (kw512) return launch_e<TX, SB, GS, EPI, 1, 512>(a, st);
+        }
+        return launch_e<TX, SB, GS, EPI, 1>(a, st);
+    }
     return launch_e<TX, SB, GS, EPI, 2>(a, st);
 }
 
