@@ -667,13 +667,20 @@ LuxStatus launch_stream_r(const QmmArgs& a, hipStream_t st) {
 // barrier publishes them while the weight loads stay in flight.
 // ---------------------------------------------------------------------------
 constexpr int kSplitMaxWaves = 8;
-constexpr int kSplitRows = 4;
+// rows per block: 8 for one row of x with codes of <= 4 bits (the block's
+// copy of x, K * sizeof(x) bytes, then serves twice the weight bytes), else 4
+// (R * MR <= 8 partials per wave, and the weight words stay in registers).
+// Measured against 4 rows, same box: K = 14336, N = 4096 9.6-9.7 us against
+// 10.0-10.2; K = 8192, N = 28672 29.4-29.9 against 32.7; f32 x, K = N = 8192
+// 17.9-18.8 against 20.7.
+constexpr bool kSplitRows8 = true;
+__host__ __device__ constexpr int split_rows(int mr, int bits) { return kSplitRows8 && mr == 1 && bits <= 4 ? 8 : 4; }
 
 // LDS bytes of the split kernel: x, a zero unit (read by idle lanes), then
 // scale and bias rows (16-byte aligned, with room for the lead of the first
 // row within its chunk), then the waves' partials
 __host__ __device__ constexpr size_t split_sb_bytes(int K, int gs, int sb_bytes) {
-    return ((size_t)kSplitRows * (K / gs) * sb_bytes + 16 + 15) & ~(size_t)15;
+    return ((size_t)8 * (K / gs) * sb_bytes + 16 + 15) & ~(size_t)15;
 }
 __host__ __device__ constexpr size_t split_lds_bytes(int mr, int K, int xe, int gs, int sb_bytes) {
     return ((size_t)mr * K + 64) * xe + 2 * split_sb_bytes(K, gs, sb_bytes) + (size_t)kSplitMaxWaves * 8 * 4;
@@ -683,7 +690,7 @@ template <int BITS, int TX, int SB, int MR, bool TWO, bool EPI>
 __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int K, int N, int gshift, int pu, Epilogue ep) {
-    constexpr int R = kSplitRows;
+    constexpr int R = split_rows(MR, BITS);
     // f16 x with 4-bit codes: the magic-number form, not the subnormal one.
     // Against the oracle's fp64 accumulation the subnormal form's error
     // grows with K (median 2.5e-6 of max|y| at K = 4096, 1e-5 at K = 14336,
@@ -836,7 +843,8 @@ LuxStatus launch_split_k(const QmmArgs& a, hipStream_t st, int ks, int pu, size_
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return LuxStatus::Internal;
     const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
-    const int blocks = (a.N + kSplitRows - 1) / kSplitRows;
+    constexpr int R = split_rows(MR, BITS);
+    const int blocks = (a.N + R - 1) / R;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * ks), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.K, a.N,
                        gshift, pu, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
