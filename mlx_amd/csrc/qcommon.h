@@ -139,8 +139,9 @@ struct MagicCfg {
     static constexpr float kPow = (float)(1u << (MANT - P));  // v(q) = 1 + q / kPow
 };
 
-// Build the 32 operand pairs of one 64-code unit.  MANT = 10 (f16) or 7 (bf16).
-template <int BITS, int MANT>
+// Build the operand pairs of NW words of codes (default: one 64-code unit,
+// 32 pairs).  MANT = 10 (f16) or 7 (bf16).
+template <int BITS, int MANT, int NW = 2 * BITS>
 __device__ __forceinline__ void unit_pairs_magic(const uint32_t* w, uint32_t* pr) {
     using C = MagicCfg<BITS, MANT>;
     constexpr uint32_t one = (MANT == 10) ? 0x3C00u : 0x3F80u;
@@ -150,7 +151,7 @@ __device__ __forceinline__ void unit_pairs_magic(const uint32_t* w, uint32_t* pr
         constexpr uint32_t m16 = ((1u << BITS) - 1u) << C::P;
         constexpr uint32_t mask = m16 | (m16 << 16);
 #pragma unroll
-        for (int wi = 0; wi < 2 * BITS; wi++) {
+        for (int wi = 0; wi < NW; wi++) {
 #pragma unroll
             for (int j = 0; j < H; j++) {
                 // code j of the low half sits at bit j*BITS; move it to P
@@ -172,7 +173,7 @@ __device__ __forceinline__ void unit_pairs_magic(const uint32_t* w, uint32_t* pr
         }
     } else {
 #pragma unroll
-        for (int p = 0; p < 32; p++) {
+        for (int p = 0; p < NW * 16 / BITS; p++) {
             uint32_t lo = unit_code<BITS>(w, 2 * p), hi = unit_code<BITS>(w, 2 * p + 1);
             pr[p] = lshl_or<MANT - BITS>(lo | (hi << 16), magic);
         }
@@ -180,10 +181,11 @@ __device__ __forceinline__ void unit_pairs_magic(const uint32_t* w, uint32_t* pr
 }
 
 // 8-bit codes as bf16 operands: q itself (exact, <= 8 significant bits),
-// natural pairing (q_{2p}, q_{2p+1}).
+// natural pairing (q_{2p}, q_{2p+1}); NW words (default one 64-code unit).
+template <int NW = 16>
 __device__ __forceinline__ void unit_pairs_bf16_u8(const uint32_t* w, uint32_t* pr) {
 #pragma unroll
-    for (int wi = 0; wi < 16; wi++) {
+    for (int wi = 0; wi < NW; wi++) {
         float f0 = (float)(w[wi] & 0xffu), f1 = (float)((w[wi] >> 8) & 0xffu);
         float f2 = (float)((w[wi] >> 16) & 0xffu), f3 = (float)(w[wi] >> 24);
         // the fp32 values are exact bf16 numbers: keep their upper halves

@@ -1,5 +1,6 @@
 // qgemv_b4.hip -- 4-bit instantiations of the GEMV kernels.
 #include "qgemv_impl.h"
+#include "qgemv_line.h"
 
 namespace lxq {
 namespace gemv {

@@ -1,5 +1,6 @@
 // qgemv_b6.hip -- 6-bit instantiations of the GEMV kernels.
 #include "qgemv_impl.h"
+#include "qgemv_line.h"
 
 namespace lxq {
 namespace gemv {

@@ -912,8 +912,18 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
     return a.has_epilogue() ? launch_t_e<BITS, TX, MR, true>(a, st) : launch_t_e<BITS, TX, MR, false>(a, st);
 }
 
+// M == 1, K <= 4096: the whole-line kernel of qgemv_line.h (defined there,
+// instantiated by the per-bit-width translation units); NotSupported for
+// shapes it does not take
+template <int BITS, int TX>
+LuxStatus launch_line(const QmmArgs& a, hipStream_t st);
+
 template <int BITS, int TX>
 LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
+    if (a.M == 1 && a.K <= 4096) {
+        const LuxStatus s = launch_line<BITS, TX>(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     if (a.M == 1 && a.K > 4096) {
         const LuxStatus s = launch_split<BITS, TX, 1>(a, st);
         if (s != LuxStatus::NotSupported) return s;

@@ -96,8 +96,11 @@ def test_quantize_bit_exact(ctx, oracle, bits, gs):
                                        (F16, F32, F32), (BF16, F16, F32)])
 def test_gemv_parity(ctx, oracle, bits, xd, sbd, od):
     O = oracle
-    for (M, K, N, gs) in [(1, 4096, 300, 64), (3, 1024, 129, 32), (8, 512, 77, 128),
-                          (5, 8192, 64, 64), (2, 192, 33, 64)]:
+    # M = 1 with K <= 4096 runs the whole-line kernel: full and partial last
+    # wave loads, an odd chunk count (K = 960), group sizes 32/64/128 (2-bit
+    # codes with group size 32: two groups per chunk), ragged N
+    for (M, K, N, gs) in [(1, 4096, 300, 64), (1, 960, 77, 32), (1, 2048, 129, 128), (1, 192, 17, 32),
+                          (3, 1024, 129, 32), (8, 512, 77, 128), (5, 8192, 64, 64), (2, 192, 33, 64)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 31 + M)
         y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
