@@ -4,16 +4,27 @@ Headline (BASELINE.json metric, configs[1] at M=1): 4-bit group-64 decode
 GEMV, K=4096, N=14336, fp16 x/scales/out.  One step = one quantized matmul
 over one weight set.  Steps rotate over 16 distinct weight copies (528 MB,
 more than twice the 256 MB Infinity Cache) so every step streams its weights
-from HBM.  value = weight bytes (packed codes + scales + biases) per step x
-steps / wall time of the timed steps, which replay a HIP graph of 16 steps
-captured on the plugin's stream (launch overhead out of the loop, work not).
+from HBM.  The timed region is exactly --steps launches issued back to back
+on the plugin's stream, bracketed by a synchronize on both sides:
+value = weight bytes (packed codes + scales + biases) x steps / host wall time
+of the region.
 
-roofline: the GEMV kernel's average duration, from HIP event pairs around
-individual launches on the plugin's stream, against the 8 TB/s HBM peak.
-gemm: configs[3] (M=2048, K=4096, N=4096 and 14336, bf16) TFLOP/s against
-the 2.5 PFLOP/s bf16 dense MFMA peak, when the GEMM path is available.
-cpu_baseline: the oracle's OpenMP quantized GEMV (a port, not the
-reference, which has no such op) on the host cores, same shape, ~10 s sample.
+roofline: HIP events on the plugin's stream around the same timed region give
+the average launch duration (kernel plus the gap to the next launch);
+achieved = algorithmic weight bytes / that duration, against 8 TB/s.  The
+same launches replayed as 16-launch HIP graphs are reported beside it.
+ceiling: an empty kernel and a plain read of the same 33 030 144 bytes (the
+fastest single-launch read pattern measured), timed the same way: what one
+launch of this size can show at all on this box.
+decode_m4_m8: configs[1] at M=4 and M=8.  gemm_m2048: configs[3] (M=2048,
+K=4096, N=4096 and 14336, bf16) TFLOP/s against the 2.5 PFLOP/s bf16 dense
+MFMA peak.
+cpu_baseline: the oracle's OpenMP quantized GEMV (a port: the reference has
+no quantized op) on all of this process's host cores and on one, plus the
+reference's own composition (host dequantize, then the reference CPU
+backend's op_matmul_f32 built from its source into oracle/_ref/); the same
+leg also uses the oracle as the checker of the GPU outputs (parity:
+max|d|/max|y| of c1, c2 and c3).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm]
 """
@@ -34,6 +45,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 F16, BF16, F32 = 1, 2, 0
+COPIES = 16
 
 
 class Hip:
@@ -84,8 +96,45 @@ class Hip:
         self.ck(self.L.hipMalloc(ctypes.byref(p), ctypes.c_size_t(nbytes)), "hipMalloc")
         return p
 
+    def memset(self, p, value, nbytes):
+        self.ck(self.L.hipMemset(p, value, ctypes.c_size_t(nbytes)), "hipMemset")
+
     def free(self, p):
         self.ck(self.L.hipFree(p), "hipFree")
+
+
+def time_launches(hip, stream, step, steps, warmup):
+    """`warmup` untimed launches, then exactly `steps` launches back to back
+    on `stream` between a synchronize on each side; returns host wall time of
+    the region and the HIP-event time per launch.  step(i) enqueues launch i
+    (rotating over the weight copies itself)."""
+    for i in range(warmup):
+        step(i)
+    hip.sync(stream)
+    e0, e1 = hip.event(), hip.event()
+    hip.sync(stream)
+    t0 = time.perf_counter()
+    hip.record(e0, stream)
+    for i in range(steps):
+        step(i)
+    hip.record(e1, stream)
+    hip.sync(stream)
+    wall = time.perf_counter() - t0
+    return {"wall_s": wall, "event_ms_per_launch": hip.elapsed_ms(e0, e1) / steps}
+
+
+def time_graph(hip, stream, step, reps=32):
+    """The same launches replayed as COPIES-launch graphs: per launch."""
+    graph = hip.capture(stream, lambda: [step(i) for i in range(COPIES)])
+    hip.launch(graph, stream)
+    hip.sync(stream)
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, stream)
+    for _ in range(reps):
+        hip.launch(graph, stream)
+    hip.record(e1, stream)
+    hip.sync(stream)
+    return hip.elapsed_ms(e0, e1) / (reps * COPIES)
 
 
 def calibrate_copy(hip, nbytes, reps=8):
@@ -93,7 +142,7 @@ def calibrate_copy(hip, nbytes, reps=8):
     kernel), the known-size reference that scales the FETCH_SIZE/WRITE_SIZE
     counters of the profiled kernels to bytes."""
     src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
-    hip.ck(hip.L.hipMemset(src, 0x5A, ctypes.c_size_t(nbytes)), "hipMemset")
+    hip.memset(src, 0x5A, nbytes)
     hip.ck(hip.L.hipDeviceSynchronize(), "hipDeviceSynchronize")
     for _ in range(reps):
         hip.ck(hip.L.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3), "hipMemcpy D2D")
@@ -128,17 +177,23 @@ def weight_bytes(N, K, bits, gs, sb):
     return N * K * bits // 8 + 2 * N * (K // gs) * (4 if sb == F32 else 2)
 
 
-def bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, kernel, copies=16, seed=1):
-    from mlx_amd import runtime
+def x_host(M, K, xd, seed):
     rng = np.random.default_rng(seed + 7)
     x32 = rng.standard_normal(M * K, dtype=np.float32).reshape(M, K)
     if xd == F16:
-        xh = x32.astype(np.float16).view(np.uint16)
-    elif xd == BF16:
+        return x32.astype(np.float16).view(np.uint16)
+    if xd == BF16:
         u = x32.view(np.uint32)
-        xh = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    else:
-        xh = x32
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return x32
+
+
+def bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, kernel, copies=COPIES, seed=1,
+              keep=False):
+    """Times `steps` launches over `copies` rotating weight sets; keep=True
+    also returns copy 0's inputs and output (downloaded) for the parity check."""
+    from mlx_amd import runtime
+    xh = x_host(M, K, xd, seed)
     xb = ctx.upload(xh)
     sets = make_weights(ctx, N, K, bits, gs, sbd, copies, seed)
     out = ctx.alloc(M * N * runtime.esize(od))
@@ -148,84 +203,193 @@ def bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, kernel, c
         wq, s, b = sets[i % copies]
         ctx.quantized_matmul(xb, wq, s, b, out, M, K, N, gs, bits, xd, sbd, od, kernel)
 
-    for i in range(max(warmup, copies)):
-        step(i)
-    ctx.sync()
-
-    # per-launch kernel duration: HIP event pairs around single launches
-    n_ev = min(64, max(steps, copies))
-    evs = [(hip.event(), hip.event()) for _ in range(n_ev)]
-    for i, (a, b) in enumerate(evs):
-        hip.record(a, stream)
-        step(i)
-        hip.record(b, stream)
-    ctx.sync()
-    kern_ms = [hip.elapsed_ms(a, b) for a, b in evs]
-    kern_ms.sort()
-    kern_avg = float(np.mean(kern_ms))
-
-    # whole job: replay a graph of `copies` steps
-    graph = hip.capture(stream, lambda: [step(i) for i in range(copies)])
-    reps = max(1, steps // copies)
-    hip.launch(graph, stream)
-    hip.sync(stream)
-    e0, e1 = hip.event(), hip.event()
-    t0 = time.perf_counter()
-    hip.record(e0, stream)
-    for _ in range(reps):
-        hip.launch(graph, stream)
-    hip.record(e1, stream)
-    hip.sync(stream)
-    wall = time.perf_counter() - t0
-    n_steps = reps * copies
-    graph_ms = hip.elapsed_ms(e0, e1) / n_steps
-
+    r = time_launches(hip, stream, step, steps, max(warmup, copies))
+    r["graph_ms_per_launch"] = time_graph(hip, stream, step)
+    r["steps"] = steps
+    if keep:
+        step(0)
+        ctx.sync()
+        r["y"] = out.download(runtime.np_dtype(od), (M, N))
+        r["x"] = xh
+        wq, s, b = sets[0]
+        sbnp = runtime.np_dtype(sbd)
+        r["w_q"] = wq.download(np.uint32, (N, K * bits // 32))
+        r["s"] = s.download(sbnp, (N, K // gs))
+        r["b"] = b.download(sbnp, (N, K // gs))
     for t in [xb, out] + [b for st in sets for b in st]:
         t.free()
-    # kernel_ms_avg: events around the graph replays on the plugin's stream,
-    # per step (kernel time plus the small gaps between graph nodes);
-    # single_ms_*: event pairs around single eager launches (adds event overhead)
-    return {"steps": n_steps, "wall_s": wall, "ms_per_step": wall * 1e3 / n_steps,
-            "kernel_ms_avg": graph_ms, "single_ms_avg": kern_avg,
-            "single_ms_median": kern_ms[len(kern_ms) // 2]}
+    return r
 
 
-def cpu_baseline(M, K, N, bits, gs, budget_s=10.0):
-    """The oracle's OpenMP GEMV on this host's cores, same shape, ~budget_s."""
-    from oracle import oracle as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, F16, F16, seed=1)
-    O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F16, F16, F16, variant="omp", threads=threads)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F16, F16, F16, variant="omp",
-                           threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    gbs = weight_bytes(N, K, bits, gs, F16) * n / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} calls of the OpenMP CPU quantized GEMV (oracle), M={M} K={K} N={N} "
-                      f"{bits}-bit g{gs} f16, {el:.1f} s"}
+# ---- ceiling leg -----------------------------------------------------------
+
+def ceiling_lib():
+    path = os.path.join(ROOT, "mlx_amd", "lib", "libluxgpu_ceiling.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run python -c 'import __graft_entry__ as g; g.build()'")
+    L = ctypes.CDLL(path)
+    L.lux_ceiling_empty.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    L.lux_ceiling_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    return L
 
 
-GEMV_PROFILE = os.path.join(ROOT, "profiles", "qgemv_m1_k4096_n14336_4bit_g64_f16.md")
-
-
-def profiled_traffic(path):
-    """HBM bytes per launch of the headline kernel: FETCH_SIZE + WRITE_SIZE
-    from two rocprofv3 --pmc runs of this script, each scaled by the same
-    counter's reading for a plain copy of known size (the summary under
-    profiles/ gives the commands and the factors).  None when absent."""
+def ceiling_leg(ctx, hip, nbytes, steps, warmup, blocks):
+    """Empty kernel (`blocks` blocks) and a plain read of nbytes over COPIES
+    rotating buffers, timed as the GEMV is."""
+    L = ceiling_lib()
+    stream = ctx.stream
+    stride = (nbytes + (2 << 20) - 1) // (2 << 20) * (2 << 20)
+    buf = hip.malloc(stride * COPIES)
+    sink = hip.malloc(1 << 20)
+    hip.memset(buf, 0x3C, stride * COPIES)
+    base = buf.value
+    out = {}
     try:
-        with open(path) as f:
+        def read(i):
+            hip.ck(L.lux_ceiling_read(ctypes.c_void_p(base + (i % COPIES) * stride), nbytes, sink,
+                                      ctypes.c_void_p(stream)), "lux_ceiling_read")
+
+        def empty(i):
+            hip.ck(L.lux_ceiling_empty(blocks, sink, ctypes.c_void_p(stream)), "lux_ceiling_empty")
+
+        for name, fn in (("empty", empty), ("read", read)):
+            r = time_launches(hip, stream, fn, steps, warmup)
+            g = time_graph(hip, stream, fn)
+            us = r["event_ms_per_launch"] * 1e3
+            out[name] = {"us_per_launch": round(us, 3), "graph_us_per_launch": round(g * 1e3, 3)}
+            if name == "read":
+                out[name]["frac_of_peak"] = round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                out[name]["graph_frac_of_peak"] = round(nbytes / g / 1e6 / HBM_PEAK_GBS, 4)
+        out["bytes"] = nbytes
+        out["empty_blocks"] = blocks
+    finally:
+        hip.sync(stream)
+        hip.free(buf)
+        hip.free(sink)
+    return out
+
+
+# ---- CPU baseline and parity (the oracle as checker) ----------------------
+
+def host_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
     except OSError:
         pass
-    return None
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"nproc": usable, "cpu_count": os.cpu_count(), "model": model,
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+
+
+def _timed(fn, budget_s, min_calls=3):
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and n >= min_calls:
+            return n, el
+
+
+def ref_cpu_backend():
+    """The reference CPU backend built from its source (oracle/_ref), or None."""
+    path = os.path.join(ROOT, "oracle", "_ref", "libref_cpu_backend.so")
+    if not os.path.exists(path):
+        return None
+    from mlx_amd import abi
+    lib = ctypes.CDLL(path)
+    desc = abi.BackendDesc()
+    if not abi.INIT_FN(("cpu_backend_init", lib))(ctypes.byref(desc)):
+        return None
+    return lib, desc
+
+
+def cpu_baseline(M, K, N, bits, gs, budget_s=4.0):
+    """The oracle's OpenMP GEMV (a port of the path: the reference has no
+    quantized op) on all of this process's cores and on one core, plus the
+    reference's own composition: host dequantize (the oracle) to f32 W^T
+    [K, N], then the reference CPU backend's op_matmul_f32 (naive, OpenMP)."""
+    from oracle import oracle as O
+    info = host_info()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or info["nproc"] or 1
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, F16, F16, seed=1)
+    wb = weight_bytes(N, K, bits, gs, F16)
+
+    def port(t):
+        return lambda: O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F16, F16, F16, variant="omp", threads=t)
+
+    n_all, el_all = _timed(port(threads), budget_s)
+    n_one, el_one = _timed(port(1), budget_s)
+    out = {"value": round(wb * n_all / el_all / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{n_all} calls of the OpenMP CPU quantized GEMV (oracle), M={M} K={K} N={N} "
+                     f"{bits}-bit g{gs} f16, {el_all:.1f} s on {threads} threads",
+           "one_core": {"value": round(wb * n_one / el_one / 1e9, 3), "unit": "GB/s", "cores": 1,
+                        "sample": f"{n_one} calls, {el_one:.1f} s"},
+           "host": info}
+    ref = ref_cpu_backend()
+    if ref is None:
+        out["reference_composition"] = None
+    else:
+        _, desc = ref
+        vt = desc.vtbl.contents
+        ctx = vt.create_context(0)
+        xf = np.ascontiguousarray(O.to_f32(x, F16))
+        bx = vt.buffer_alloc_with_data(ctx, xf.ctypes.data, xf.nbytes)
+        bw = vt.buffer_alloc(ctx, K * N * 4)
+        by = vt.buffer_alloc(ctx, M * N * 4)
+
+        def compose():
+            wt = np.ascontiguousarray(O.dequantize(w_q, s, b, K, gs, bits, F16).T)
+            if vt.buffer_copy_from_host(ctx, bw, wt.ctypes.data, wt.nbytes) != 0:
+                raise RuntimeError("reference buffer_copy_from_host")
+            if vt.op_matmul_f32(ctx, bx, bw, by, M, K, N) != 0:
+                raise RuntimeError("reference op_matmul_f32")
+
+        n_ref, el_ref = _timed(compose, budget_s, min_calls=2)
+        for h in (bx, bw, by):
+            vt.buffer_free(ctx, h)
+        vt.destroy_context(ctx)
+        out["reference_composition"] = {
+            "value": round(wb * n_ref / el_ref / 1e9, 3), "unit": "GB/s", "kind": "reference",
+            "cores": int(os.environ.get("OMP_NUM_THREADS", "0")) or info["nproc"],
+            "sample": f"{n_ref} calls of host dequantize to f32 W^T + reference cpu_op_matmul_f32 "
+                      f"(src/cpu_backend.cpp:243-266, OpenMP), {el_ref:.1f} s"}
+    return out
+
+
+def rel_err(y, want, od):
+    from oracle import oracle as O
+    yf = O.to_f32(y, od).astype(np.float64) if od != F32 else y.astype(np.float64)
+    wf = O.to_f32(want, od).astype(np.float64) if od != F32 else want.astype(np.float64)
+    return float(np.abs(yf - wf).max() / max(np.abs(wf).max(), 1e-30))
+
+
+def parity(cases, threads):
+    """max|d|/max|y| of each GPU output against the oracle (the oracle's
+    OpenMP form, fp32 accumulation) on the same inputs; GEMM outputs also
+    against the exact-weight form."""
+    from oracle import oracle as O
+    res = {}
+    for name, c in cases.items():
+        M, K, N, gs, bits, xd, sbd, od, gemm = c["shape"]
+        r = c["run"]
+        args = (r["x"], r["w_q"], r["s"], r["b"], M, K, N, gs, bits, xd, sbd)
+        want = O.quantized_matmul(*args, od, variant="omp", threads=threads, w_round=xd if gemm else F32)
+        e = {"max_rel": rel_err(r["y"], want, od), "out_dtype": {F16: "f16", BF16: "bf16", F32: "f32"}[od]}
+        if gemm:
+            exact = O.quantized_matmul(*args, od, variant="omp", threads=threads)
+            e["max_rel_vs_exact_weights"] = rel_err(r["y"], exact, od)
+        res[name] = e
+    return res
 
 
 # (name, M, K, N, bits, group, x dtype, scale dtype, out dtype)
@@ -244,49 +408,74 @@ SWEEP = [
 ]
 
 
-def sweep(ctx, hip, steps):
-    """One line per config: kernel AUTO picks, graph-replay time per launch,
-    weight GB/s and TFLOP/s with their roofline fractions."""
+def sweep(ctx, hip, steps, only=None):
+    """One line per config: kernel AUTO picks, per-launch time (stream and
+    graph replays), weight GB/s and TFLOP/s with their roofline fractions."""
     from mlx_amd import abi
     names = {abi.KERNEL_GEMV: "gemv", abi.KERNEL_GEMM: "gemm"}
     for name, M, K, N, bits, gs, xd, sbd, od in SWEEP:
+        if only and name not in only:
+            continue
         kern = ctx.select_kernel(M, K, N, gs, bits, xd, sbd)
-        copies = 4 if M >= 256 else 16
+        copies = 4 if M >= 256 else COPIES
         r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, 8, abi.KERNEL_AUTO, copies=copies)
-        t = r["kernel_ms_avg"] * 1e-3
+        t = r["event_ms_per_launch"] * 1e-3
         wb = weight_bytes(N, K, bits, gs, sbd)
         flops = 2.0 * M * N * K
         print(json.dumps({"config": name, "M": M, "K": K, "N": N, "bits": bits, "group_size": gs,
                           "kernel": names.get(kern, str(kern)), "us": round(t * 1e6, 3),
+                          "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                           "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
                           "tflops": round(flops / t / 1e12, 2),
                           "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4)}), flush=True)
 
 
-def decode_legs(ctx, hip, K, N, bits, gs, steps):
+def decode_legs(ctx, hip, K, N, bits, gs, steps, warmup):
     """configs[1] at M=4 and M=8: same weight bytes as M=1, 4x / 8x the math."""
     from mlx_amd import abi
     out = {}
     wb = weight_bytes(N, K, bits, gs, F16)
     for m in (4, 8):
-        r = bench_qmm(ctx, hip, m, K, N, bits, gs, F16, F16, F16, min(steps, 1024), 16, abi.KERNEL_AUTO)
-        t = r["kernel_ms_avg"] * 1e-3
-        out[f"M{m}"] = {"kernel_us_avg": round(t * 1e6, 3), "weight_GBs": round(wb / t / 1e9, 1),
-                        "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4)}
+        r = bench_qmm(ctx, hip, m, K, N, bits, gs, F16, F16, F16, steps, warmup, abi.KERNEL_AUTO)
+        t = r["event_ms_per_launch"] * 1e-3
+        out[f"M{m}"] = {"kernel_us_avg": round(t * 1e6, 3), "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
+                        "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4)}
     return out
+
+
+GEMV_PROFILE = os.path.join(ROOT, "profiles", "qgemv_line_m1_k4096_n14336_4bit_g64_f16.md")
+
+
+def profiled_traffic(path):
+    """HBM bytes per launch of the headline kernel: FETCH_SIZE + WRITE_SIZE
+    from two rocprofv3 --pmc runs of this script, each scaled by the same
+    counter's reading for a plain copy of known size (the summary under
+    profiles/ gives the commands and the factors).  None when absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4096)
+    ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and parity leg")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true")
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE config")
+    ap.add_argument("--only", default="", help="with --sweep: comma-separated config names (c0..c4)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the configs[1] M=4 and M=8 decode legs (for profiling)")
+    ap.add_argument("--ceiling-only", action="store_true", help="only the ceiling leg (for profiling)")
+    ap.add_argument("--gemm-only", action="store_true", help="only the configs[3] GEMM legs (for profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a device-to-device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -295,28 +484,56 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(the plugin path is single-device; see DESIGN.md for how it would shard)",
+              "(the plugin path is single-device; DESIGN.md section 7 gives how it would shard)",
               file=sys.stderr)
         sys.exit(2)
 
     from mlx_amd import abi, runtime
     hip = Hip()
     ctx = runtime.Context(0)
+    M, K, N, bits, gs = 1, 4096, 14336, 4, 64
+    wb = weight_bytes(N, K, bits, gs, F16)
     if args.sweep:
-        sweep(ctx, hip, min(args.steps, 256))
+        sweep(ctx, hip, min(args.steps, 256), [s for s in args.only.split(",") if s])
+        ctx.close()
+        return
+    if args.decode_only:
+        print(json.dumps({"decode_m4_m8": decode_legs(ctx, hip, K, N, bits, gs, args.steps, args.warmup)}),
+              flush=True)
+        ctx.close()
+        return
+    if args.ceiling_only:
+        print(json.dumps({"ceiling": ceiling_leg(ctx, hip, wb, args.steps, args.warmup, 512)}), flush=True)
         ctx.close()
         return
 
-    M, K, N, bits, gs = 1, 4096, 14336, 4, 64
-    if args.decode_only:
-        print(json.dumps({"decode_m4_m8": decode_legs(ctx, hip, K, N, bits, gs, args.steps)}), flush=True)
+    def gemm_legs(keep):
+        gemm, runs = {}, {}
+        for n in (4096, 14336):
+            if ctx.select_kernel(2048, 4096, n, 64, 4, BF16) != abi.KERNEL_GEMM:
+                break
+            steps = min(args.steps, 256)
+            rg = bench_qmm(ctx, hip, 2048, 4096, n, 4, 64, BF16, BF16, BF16, steps, 8, abi.KERNEL_AUTO,
+                           copies=4, keep=keep and n == 4096)
+            flops = 2.0 * 2048 * 4096 * n
+            tf = flops / (rg["event_ms_per_launch"] * 1e-3) / 1e12
+            gemm[f"N{n}"] = {"tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                             "kernel_us_avg": round(rg["event_ms_per_launch"] * 1e3, 2),
+                             "graph_us": round(rg["graph_ms_per_launch"] * 1e3, 2),
+                             "wall_tflops": round(flops * rg["steps"] / rg["wall_s"] / 1e12, 2)}
+            runs[n] = rg
+        return gemm, runs
+
+    if args.gemm_only:
+        print(json.dumps({"gemm_m2048": gemm_legs(False)[0]}), flush=True)
         ctx.close()
         return
-    r = bench_qmm(ctx, hip, M, K, N, bits, gs, F16, F16, F16, args.steps, args.warmup,
-                  abi.KERNEL_AUTO)
-    wb = weight_bytes(N, K, bits, gs, F16)
+
+    keep = not args.no_cpu
+    r = bench_qmm(ctx, hip, M, K, N, bits, gs, F16, F16, F16, args.steps, args.warmup, abi.KERNEL_AUTO, keep=keep)
     value = wb * r["steps"] / r["wall_s"] / 1e9
-    achieved = wb / (r["kernel_ms_avg"] * 1e-3) / 1e9
+    t = r["event_ms_per_launch"] * 1e-3
+    achieved = wb / t / 1e9
     line = {
         "metric": "weight GB/s (%HBM peak) at M=1 & TFLOP/s (%MFMA peak) at M=2048, 4-bit",
         "value": round(value, 2),
@@ -324,7 +541,7 @@ def main():
         "n_gpus": 1,
         "steps": r["steps"],
         "warmup": args.warmup,
-        "ms_per_step": round(r["ms_per_step"], 6),
+        "ms_per_step": round(r["wall_s"] * 1e3 / r["steps"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -336,27 +553,37 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(GEMV_PROFILE),
-                     "kernel": "qgemv_stream_kernel", "kernel_us_avg": round(r["kernel_ms_avg"] * 1e3, 3),
-                     "kernel_us_single_launch": round(r["single_ms_avg"] * 1e3, 3),
-                     "algorithmic_bytes": wb},
+                     "kernel": "qgemv_line_kernel", "kernel_us_avg": round(t * 1e6, 3),
+                     "graph_us_per_launch": round(r["graph_ms_per_launch"] * 1e3, 3),
+                     "graph_frac": round(wb / r["graph_ms_per_launch"] / 1e6 / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": wb, "timing": "HIP events around the timed launches on the plugin stream"},
     }
-    line["decode_m4_m8"] = decode_legs(ctx, hip, K, N, bits, gs, args.steps)
+    if not args.no_ceiling:
+        line["ceiling"] = ceiling_leg(ctx, hip, wb, args.steps, args.warmup, 512)
+    line["decode_m4_m8"] = decode_legs(ctx, hip, K, N, bits, gs, min(args.steps, 1024), args.warmup)
+    gemm_runs = {}
     if not args.no_gemm:
-        gemm = {}
-        for n in (4096, 14336):
-            if ctx.select_kernel(2048, 4096, n, 64, 4, BF16) != abi.KERNEL_GEMM:
-                break
-            rg = bench_qmm(ctx, hip, 2048, 4096, n, 4, 64, BF16, BF16, BF16, min(args.steps, 256),
-                           8, abi.KERNEL_AUTO, copies=4)
-            flops = 2.0 * 2048 * 4096 * n
-            tf = flops / (rg["kernel_ms_avg"] * 1e-3) / 1e12
-            gemm[f"N{n}"] = {"tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                             "kernel_us_avg": round(rg["kernel_ms_avg"] * 1e3, 2),
-                             "wall_tflops": round(flops * rg["steps"] / rg["wall_s"] / 1e12, 2)}
-        line["gemm_m2048"] = gemm or None
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(M, K, N, bits, gs)
+        line["gemm_m2048"], gemm_runs = gemm_legs(keep)
+    c2 = None
+    # c2's kernel family decides its semantics (the GEMM kernels dequantize
+    # to the activation type before the multiply)
+    c2_gemm = ctx.select_kernel(32, 8192, 8192, 128, 8, BF16) == abi.KERNEL_GEMM
+    if keep:
+        c2 = bench_qmm(ctx, hip, 32, 8192, 8192, 8, 128, BF16, BF16, BF16, 64, 8, abi.KERNEL_AUTO,
+                       copies=4, keep=True)
+        c2f = bench_qmm(ctx, hip, 32, 8192, 8192, 8, 128, BF16, BF16, F32, 16, 4, abi.KERNEL_AUTO,
+                        copies=4, keep=True)
     ctx.close()
+    if keep:
+        cb = cpu_baseline(M, K, N, bits, gs)
+        cases = {"c1_m1_f16": {"shape": (M, K, N, gs, bits, F16, F16, F16, False), "run": r},
+                 "c2_bf16": {"shape": (32, 8192, 8192, 128, 8, BF16, BF16, BF16, c2_gemm), "run": c2},
+                 "c2_f32out": {"shape": (32, 8192, 8192, 128, 8, BF16, BF16, F32, c2_gemm), "run": c2f}}
+        if 4096 in gemm_runs:
+            cases["c3_n4096_bf16"] = {"shape": (2048, 4096, 4096, 64, 4, BF16, BF16, BF16, True),
+                                      "run": gemm_runs[4096]}
+        cb["parity"] = parity(cases, cb["cores"])
+        line["cpu_baseline"] = cb
     print(json.dumps(line), flush=True)
 
 

@@ -22,6 +22,9 @@ LIBDIR = os.path.join(PKG, "lib")
 PLUGIN = os.path.join(LIBDIR, "libluxgpu_backend_hip.so")
 CORE = os.path.join(LIBDIR, "libluxgpu_quant_core.so")
 CORE_SRC = os.path.join(CSRC, "core", "lux_quant_core.cpp")
+# bench.py's ceiling leg (empty kernel, plain read): its own library, not the plugin
+CEILING = os.path.join(LIBDIR, "libluxgpu_ceiling.so")
+CEILING_SRC = os.path.join(CSRC, "probe", "ceiling.hip")
 ARCH = os.environ.get("LUX_HIP_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -70,8 +73,9 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, PLUGIN)
     build_core()
+    build_ceiling()
     if verbose:
-        print(f"built {PLUGIN} and {CORE}", file=sys.stderr)
+        print(f"built {PLUGIN}, {CORE} and {CEILING}", file=sys.stderr)
     return PLUGIN
 
 
@@ -85,6 +89,18 @@ def build_core() -> str:
         raise RuntimeError(f"core library build failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, CORE)
     return CORE
+
+
+def build_ceiling() -> str:
+    """bench.py's measurement kernels (csrc/probe/ceiling.hip)."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    tmp = CEILING + ".tmp"
+    cmd = [HIPCC, *CFLAGS, "-shared", CEILING_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"ceiling library build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CEILING)
+    return CEILING
 
 
 if __name__ == "__main__":

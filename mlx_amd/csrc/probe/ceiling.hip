@@ -1,0 +1,72 @@
+// ceiling.hip -- measurement kernels for bench.py's ceiling leg (gfx950).
+//
+// Built into its own library (libluxgpu_ceiling.so), not into the plugin.
+// They bound what any single launch of the decode GEMV can show on this
+// hardware, timed exactly as the GEMV is:
+//   * an empty kernel: the fixed cost of one launch (dispatch and
+//     completion), with no memory traffic;
+//   * a plain read of `bytes` bytes: every lane issues eight 128-bit loads at
+//     once (each wave instruction reads 1 KB contiguous, whole 128-byte
+//     lines) with the non-temporal cache policy, the fastest single-launch
+//     read pattern measured for 33 MB; the words are folded and stored only
+//     if they equal a value random data does not produce, so the loads stay.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+
+constexpr int kLoads = 8;          // 128-bit loads per lane
+constexpr int kThreads = 256;
+constexpr int kBlockBytes = kThreads * kLoads * 16;
+
+__global__ __launch_bounds__(kThreads) void ceiling_empty_kernel(uint32_t* sink, int never) {
+    if (never == 0x7fffffff) sink[blockIdx.x] = threadIdx.x;
+}
+
+__global__ __launch_bounds__(kThreads) void ceiling_read_kernel(const uint8_t* base, uint32_t bytes, uint32_t* sink) {
+    // offsets past `bytes` read zeros
+    const auto r = rsrc(base, bytes);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t wbase = ((uint32_t)blockIdx.x * (kThreads / 64) + wave) * kLoads * 1024u;
+    v4u32 v[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; i++) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, wbase + i * 1024 + lane * 16, 0, 2);
+    v4u32 acc = v[0];
+#pragma unroll
+    for (int i = 1; i < kLoads; i++) acc = (acc ^ v[i]) + (v[i] << 1);
+    if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0x85ebca6bu) sink[blockIdx.x] = acc.w;
+}
+
+}  // namespace
+
+extern "C" {
+
+// One launch of the empty kernel with `blocks` blocks of 256 threads on
+// `stream`; sink: any device buffer of >= 4 * blocks bytes (never written).
+// Returns the hipError_t of the launch.
+__attribute__((visibility("default"))) int lux_ceiling_empty(int blocks, void* sink, void* stream) {
+    if (blocks <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(ceiling_empty_kernel, dim3(blocks), dim3(kThreads), 0, (hipStream_t)stream,
+                       static_cast<uint32_t*>(sink), 0);
+    return (int)hipGetLastError();
+}
+
+// One launch of the plain read of `bytes` bytes at `buf` (< 2^31) on
+// `stream`; sink: a device buffer of >= 4 * ceil(bytes / 32 KiB) bytes (never
+// written in practice).  Returns the hipError_t of the launch.
+__attribute__((visibility("default"))) int lux_ceiling_read(const void* buf, uint64_t bytes, void* sink,
+                                                            void* stream) {
+    if (buf == nullptr || bytes == 0 || bytes >= (1ull << 31)) return (int)hipErrorInvalidValue;
+    const int blocks = (int)((bytes + kBlockBytes - 1) / kBlockBytes);
+    hipLaunchKernelGGL(ceiling_read_kernel, dim3(blocks), dim3(kThreads), 0, (hipStream_t)stream,
+                       static_cast<const uint8_t*>(buf), (uint32_t)bytes, static_cast<uint32_t*>(sink));
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"
