@@ -9,6 +9,18 @@ size_t gemv_lds_bytes(int MR, int K, int x_dtype) {
     return (size_t)MR * (K / 64) * stride * elem + (size_t)MR * (K / 32) * 4;
 }
 
+static LuxStatus launch_bits(const QmmArgs& a, hipStream_t st) {
+    switch (a.bits) {
+    case 2: return launch_b<2>(a, st);
+    case 3: return launch_b<3>(a, st);
+    case 4: return launch_b<4>(a, st);
+    case 5: return launch_b<5>(a, st);
+    case 6: return launch_b<6>(a, st);
+    case 8: return launch_b<8>(a, st);
+    default: return LuxStatus::NotSupported;
+    }
+}
+
 // M is processed in chunks of up to 8 rows of x, as many as the staged x
 // fits in 64 KB of LDS (two blocks per CU).
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
@@ -41,6 +53,13 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const LuxStatus s = launch_qmm_skinny(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
+    // one or two rows of x: the whole-line, stream and split-K kernels take
+    // them whole (the split-K kernel stages both x rows itself, up to
+    // K = 16384); only if they decline, the chunked row-run kernel below
+    if (args.M <= 2) {
+        const LuxStatus s = launch_bits(args, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     int chunk = 8;
     while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
     // one row of x may still run on the split-K stream kernel (K <= 32768),
@@ -52,16 +71,7 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const size_t xel = args.x_dtype == DT_F32 ? 4 : 2, yel = args.out_dtype == DT_F32 ? 4 : 2;
         a.x = static_cast<const uint8_t*>(args.x) + (size_t)m0 * args.K * xel;
         a.y = static_cast<uint8_t*>(args.y) + (size_t)m0 * args.N * yel;
-        LuxStatus s;
-        switch (a.bits) {
-        case 2: s = launch_b<2>(a, st); break;
-        case 3: s = launch_b<3>(a, st); break;
-        case 4: s = launch_b<4>(a, st); break;
-        case 5: s = launch_b<5>(a, st); break;
-        case 6: s = launch_b<6>(a, st); break;
-        case 8: s = launch_b<8>(a, st); break;
-        default: return LuxStatus::NotSupported;
-        }
+        const LuxStatus s = launch_bits(a, st);
         if (s != LuxStatus::Ok) return s;
     }
     return LuxStatus::Ok;

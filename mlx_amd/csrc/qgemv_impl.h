@@ -676,21 +676,23 @@ constexpr int kSplitMaxWaves = 8;
 constexpr bool kSplitRows8 = true;
 __host__ __device__ constexpr int split_rows(int mr, int bits) { return kSplitRows8 && mr == 1 && bits <= 4 ? 8 : 4; }
 
-// LDS bytes of the split kernel: x, a zero unit (read by idle lanes), then
-// scale and bias rows (16-byte aligned, with room for the lead of the first
-// row within its chunk), then the waves' partials
-__host__ __device__ constexpr size_t split_sb_bytes(int K, int gs, int sb_bytes) {
-    return ((size_t)8 * (K / gs) * sb_bytes + 16 + 15) & ~(size_t)15;
+// LDS bytes of the split kernel with R rows per block: x, a zero unit (read
+// by idle lanes), then the R scale and R bias rows (16-byte aligned, with
+// room for the lead of the first row within its chunk), then the waves'
+// partials
+__host__ __device__ constexpr size_t split_sb_bytes(int R, int K, int gs, int sb_bytes) {
+    return ((size_t)R * (K / gs) * sb_bytes + 16 + 15) & ~(size_t)15;
 }
-__host__ __device__ constexpr size_t split_lds_bytes(int mr, int K, int xe, int gs, int sb_bytes) {
-    return ((size_t)mr * K + 64) * xe + 2 * split_sb_bytes(K, gs, sb_bytes) + (size_t)kSplitMaxWaves * 8 * 4;
+__host__ __device__ constexpr size_t split_lds_bytes(int mr, int R, int K, int xe, int gs, int sb_bytes) {
+    return ((size_t)mr * K + 64) * xe + 2 * split_sb_bytes(R, K, gs, sb_bytes) + (size_t)kSplitMaxWaves * 8 * 4;
 }
 
-template <int BITS, int TX, int SB, int MR, bool TWO, bool EPI>
+// R: rows per block, split_rows(MR, BITS), or 4 where 8 rows of scales do
+// not fit the LDS (f32 x and scales at the largest K)
+template <int BITS, int TX, int SB, int MR, int R, bool TWO, bool EPI>
 __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int K, int N, int gshift, int pu, Epilogue ep) {
-    constexpr int R = split_rows(MR, BITS);
     // f16 x with 4-bit codes: the magic-number form, not the subnormal one.
     // Against the oracle's fp64 accumulation the subnormal form's error
     // grows with K (median 2.5e-6 of max|y| at K = 4096, 1e-5 at K = 14336,
@@ -711,7 +713,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const uint32_t sb_row = (uint32_t)G * kSb;
     const int n0 = blockIdx.x * R;
-    const size_t sbb = split_sb_bytes(K, 1 << gshift, kSb);
+    const size_t sbb = split_sb_bytes(R, K, 1 << gshift, kSb);
     uint8_t* const lx = lds;
     uint8_t* const lzero = lds + (size_t)MR * K * XE;  // one unit of zeros
     uint8_t* const lsd = lzero + 64 * XE;
@@ -834,20 +836,31 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
     }
 }
 
-template <int BITS, int TX, int SB, int MR, bool TWO, bool EPI>
+template <int BITS, int TX, int SB, int MR, int R, bool TWO, bool EPI>
 LuxStatus launch_split_k(const QmmArgs& a, hipStream_t st, int ks, int pu, size_t lds) {
-    auto kern = qgemv_split_kernel<BITS, TX, SB, MR, TWO, EPI>;
+    auto kern = qgemv_split_kernel<BITS, TX, SB, MR, R, TWO, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return LuxStatus::Internal;
     const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
-    constexpr int R = split_rows(MR, BITS);
     const int blocks = (a.N + R - 1) / R;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * ks), lds, st, a.x, a.wq, a.scales, a.biases, a.y, a.K, a.N,
                        gshift, pu, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+// one block's scale rows and its weight rows (relative to the block's first
+// row) stay far below 2^31; x is below 128 KB
+template <int BITS, int TX, int SB, int MR, int R>
+LuxStatus launch_split_r(const QmmArgs& a, hipStream_t st, int ks, int pu, size_t lds) {
+    const bool epi = a.has_epilogue();
+    if (a.group_size == 32)
+        return epi ? launch_split_k<BITS, TX, SB, MR, R, true, true>(a, st, ks, pu, lds)
+                   : launch_split_k<BITS, TX, SB, MR, R, true, false>(a, st, ks, pu, lds);
+    return epi ? launch_split_k<BITS, TX, SB, MR, R, false, true>(a, st, ks, pu, lds)
+               : launch_split_k<BITS, TX, SB, MR, R, false, false>(a, st, ks, pu, lds);
 }
 
 // M == MR rows of x, 4096 < K <= 32768 (K % 64 == 0), x, scales and rows
@@ -860,16 +873,15 @@ LuxStatus launch_split_sb(const QmmArgs& a, hipStream_t st) {
     if (ks > kSplitMaxWaves) return LuxStatus::NotSupported;
     const int pu = (units + ks - 1) / ks;
     constexpr int XE = TX == DT_F32 ? 4 : 2, kSb = SB == DT_F32 ? 4 : 2;
-    const size_t lds = split_lds_bytes(MR, a.K, XE, a.group_size, kSb);
-    if (lds > 160 * 1024) return LuxStatus::NotSupported;
-    // one block's scale rows and its weight rows (relative to the block's
-    // first row) stay far below 2^31; x is below 128 KB
-    const bool epi = a.has_epilogue();
-    if (a.group_size == 32)
-        return epi ? launch_split_k<BITS, TX, SB, MR, true, true>(a, st, ks, pu, lds)
-                   : launch_split_k<BITS, TX, SB, MR, true, false>(a, st, ks, pu, lds);
-    return epi ? launch_split_k<BITS, TX, SB, MR, false, true>(a, st, ks, pu, lds)
-               : launch_split_k<BITS, TX, SB, MR, false, false>(a, st, ks, pu, lds);
+    constexpr int R = split_rows(MR, BITS);
+    const size_t lds = split_lds_bytes(MR, R, a.K, XE, a.group_size, kSb);
+    if (lds <= 160 * 1024) return launch_split_r<BITS, TX, SB, MR, R>(a, st, ks, pu, lds);
+    // 8 rows of scales do not fit (f32 x and scales at the largest K): 4 rows
+    if constexpr (R == 8) {
+        const size_t lds4 = split_lds_bytes(MR, 4, a.K, XE, a.group_size, kSb);
+        if (lds4 <= 160 * 1024) return launch_split_r<BITS, TX, SB, MR, 4>(a, st, ks, pu, lds4);
+    }
+    return LuxStatus::NotSupported;
 }
 
 template <int BITS, int TX, int MR>

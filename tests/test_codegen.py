@@ -19,7 +19,8 @@ import subprocess
 import pytest
 
 LLVM = "/opt/rocm/llvm/bin"
-KERNELS = ("qgemv_stream_kernel", "qgemv_split_kernel", "qgemv_dec_kernel")
+KERNELS = ("qgemv_stream_kernel", "qgemv_split_kernel", "qgemv_dec_kernel", "qmm_skinny_kernel")
+LINE = "qgemv_line_kernel"
 
 
 def _tool(name):
@@ -43,7 +44,7 @@ def disassembly(tmp_path_factory):
     for co in sorted(d.glob("plugin.so.*gfx950*")):
         syms = subprocess.run([objdump, "-t", str(co)], check=True, capture_output=True, text=True).stdout
         names = [ln.split()[-1] for ln in syms.splitlines()
-                 if " .text" in ln and any(k in ln for k in KERNELS) and not ln.endswith(".kd")]
+                 if " .text" in ln and any(k in ln for k in KERNELS + (LINE,)) and not ln.endswith(".kd")]
         if not names:
             continue
         dis = subprocess.run([objdump, "-d", "--mcpu=gfx950", "--disassemble-symbols=" + ",".join(names), str(co)],
@@ -63,6 +64,8 @@ def test_weight_loads_precede_their_wait(disassembly):
     found = {k: 0 for k in KERNELS}
     bad = []
     for name, lines in disassembly.items():
+        if LINE in name:
+            continue
         loads, vm = 0, None
         for t in lines:
             if t.startswith("buffer_load") and not re.search(r"\blds\b", t):
@@ -79,4 +82,34 @@ def test_weight_loads_precede_their_wait(disassembly):
         if vm is not None and loads < vm:
             bad.append(f"{name}: {loads} loads before vmcnt({vm})")
     assert all(found.values()), f"kernels not found in the plugin: {found}"
+    assert not bad, "\n".join(bad[:10])
+
+
+def test_line_kernel_issue_order(disassembly):
+    """The whole-line M = 1 kernel: x and scale loads (default cache policy)
+    all issue before the block barrier, the non-temporal code loads all after
+    it and before the first wait on a vector-memory load -- so the x and scale
+    requests of every wave precede the codes in the CU's queue, and no code
+    load was moved behind the arithmetic."""
+    seen, bad = 0, []
+    for name, lines in disassembly.items():
+        if LINE not in name:
+            continue
+        seen += 1
+        bar = next((i for i, t in enumerate(lines) if t.startswith("s_barrier")), None)
+        if bar is None:
+            bad.append(f"{name}: no barrier")
+            continue
+        before, after = lines[:bar], lines[bar:]
+        if any(t.startswith("buffer_load") and re.search(r"\bnt\b", t) for t in before):
+            bad.append(f"{name}: code load before the barrier")
+        if not any(t.startswith("buffer_load") for t in before):
+            bad.append(f"{name}: no x/scale load before the barrier")
+        wait = next((i for i, t in enumerate(after) if re.search(r"s_waitcnt\b.*\bvmcnt\(", t)), len(after))
+        late = [t for t in after[wait:] if t.startswith("buffer_load")]
+        if late:
+            bad.append(f"{name}: {len(late)} loads after the first vmcnt wait")
+        if not any(t.startswith("buffer_load") and re.search(r"\bnt\b", t) for t in after[:wait]):
+            bad.append(f"{name}: no code load between the barrier and the first wait")
+    assert seen, "qgemv_line_kernel not found in the plugin"
     assert not bad, "\n".join(bad[:10])
