@@ -23,6 +23,7 @@
 #include "../../include/lux_gpu_backend_abi.h"
 #include "../../include/lux_gpu_quant_backend.h"
 #include "kernels.h"
+#include "qdispatch.h"
 #include "qweights.h"
 
 namespace {
@@ -33,7 +34,13 @@ struct HipContext {
     char name[256] = {0};
     int compute_units = 0;
     int max_wg = 0;
+    // kernel workspace (partial sums and self-resetting tile counters of the
+    // split-K GEMM), allocated and zeroed once here so that no launch
+    // allocates; used only by work on `stream`, which orders its users
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
 };
+
 
 struct HipBuffer {
     void* ptr = nullptr;
@@ -64,11 +71,7 @@ LuxBackendError map_status(lxq::LuxStatus s) {
     }
 }
 
-bool is_gfx950(int dev) {
-    hipDeviceProp_t p;
-    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return false;
-    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
-}
+bool is_gfx950(int dev) { return lux_hip_is_gfx950(dev); }
 
 // ---------------------------------------------------------------------------
 // lifecycle, device info, sync
@@ -92,6 +95,18 @@ LuxBackendContext* hip_create_context(int device_index) {
     std::snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", p.name, p.gcnArchName);
     ctx->compute_units = p.multiProcessorCount;
     ctx->max_wg = p.maxThreadsPerBlock;
+    // without a workspace the kernels that need one are skipped
+    if (hipMalloc(&ctx->ws, lxq::kSplitWorkspaceBytes) == hipSuccess) {
+        if (hipMemset(ctx->ws, 0, lxq::kSplitWorkspaceBytes) == hipSuccess) {
+            ctx->ws_bytes = lxq::kSplitWorkspaceBytes;
+        } else {
+            hipFree(ctx->ws);
+            ctx->ws = nullptr;
+        }
+    } else {
+        (void)hipGetLastError();
+        ctx->ws = nullptr;
+    }
     return reinterpret_cast<LuxBackendContext*>(ctx);
 }
 
@@ -103,6 +118,7 @@ void hip_destroy_context(LuxBackendContext* c) {
         hipStreamSynchronize(ctx->stream);
         hipStreamDestroy(ctx->stream);
     }
+    if (ctx->ws) hipFree(ctx->ws);
     delete ctx;
 }
 
@@ -276,8 +292,9 @@ int gemv_max_m(int K, int bits, LuxBackendDtype x_dtype) {
 }
 
 // shapes the MFMA GEMMs take: 16-bit activations, and
-//  * 8 < M <= 64 with K a multiple of 1024 (small-M kernel: its 4 waves split
-//    K into parts of 4-step multiples), x and W below 2 GiB; or
+//  * 8 < M <= 64 with K a multiple of 128 (split-K small-M kernel: its
+//    super-steps are 128 codes of K; it runs unsplit without a workspace),
+//    x, W and f32 scales below 2 GiB; or
 //  * K a multiple of 256 (the large kernel's scale windows span 4 K steps of
 //    64), x and W below 4 GiB (32-bit offsets), and its LDS buffers within
 //    one CU's 160 KB (f32 scales at group size 32 with 6- or 8-bit codes do
@@ -285,8 +302,8 @@ int gemv_max_m(int K, int bits, LuxBackendDtype x_dtype) {
 bool gemm_ok(int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dtype,
              LuxBackendDtype sb_dtype) {
     if (x_dtype == LUX_DTYPE_FLOAT32) return false;
-    if (M > 8 && M <= 64 && K % 1024 == 0 && (size_t)M * K * 2 < (1ull << 31) &&
-        (size_t)N * K * bits / 8 < (1ull << 31))
+    if (M > 8 && M <= 64 && K % 128 == 0 && (size_t)M * K * 2 < (1ull << 31) &&
+        (size_t)N * K * bits / 8 < (1ull << 31) && (size_t)N * (K / 32) * 4 < (1ull << 31))
         return true;
     if (sb_dtype == LUX_DTYPE_FLOAT32 && group_size == 32 && bits >= 6) return false;
     return K % 256 == 0 && (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
@@ -299,6 +316,43 @@ LuxQuantKernel select_kernel_impl(int M, int K, int N, int group_size, int bits,
     return LUX_QMM_KERNEL_GEMM;
 }
 
+}  // namespace
+
+bool lux_hip_is_gfx950(int dev) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return false;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+LuxBackendError lux_hip_qmm_validate(int M, int K, int N, int group_size, int bits, int x_dtype, int sb_dtype,
+                                     int out_dtype, int kernel) {
+    if (M < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    LuxBackendError e = check_format(K, N, group_size, bits);
+    if (e != LUX_BACKEND_OK) return e;
+    if (!dtype_ok(x_dtype) || !dtype_ok(sb_dtype) || !dtype_ok(out_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+    if (kernel != LUX_QMM_KERNEL_AUTO && kernel != LUX_QMM_KERNEL_GEMV && kernel != LUX_QMM_KERNEL_GEMM)
+        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    return LUX_BACKEND_OK;
+}
+
+LuxBackendError lux_hip_qmm_dispatch(const lxq::QmmArgs& a, int kernel, hipStream_t st) {
+    const LuxBackendDtype xd = (LuxBackendDtype)a.x_dtype, sd = (LuxBackendDtype)a.sb_dtype;
+    if (kernel == LUX_QMM_KERNEL_AUTO) kernel = select_kernel_impl(a.M, a.K, a.N, a.group_size, a.bits, xd, sd);
+    if (kernel == LUX_QMM_KERNEL_GEMM) {
+        // an explicit GEMM request runs the GEMM or fails: its numerics
+        // (weights rounded to the activation type) differ from the GEMV's
+        if (!gemm_ok(a.M, a.K, a.N, a.group_size, a.bits, xd, sd)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+        return map_status(lxq::launch_qgemm(a, st));
+    }
+    if (a.K % 64 == 0) {
+        lxq::LuxStatus s = lxq::launch_qgemv(a, st);
+        if (s != lxq::LuxStatus::NotSupported) return map_status(s);
+    }
+    return map_status(lxq::launch_qmm_generic(a, st));
+}
+
+namespace {
+
 LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBuffer* w_q,
                          LuxBackendBuffer* scales, LuxBackendBuffer* biases,
                          LuxBackendBuffer* out, int M, int K, int N, int group_size, int bits,
@@ -309,13 +363,9 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     HipContext* ctx = C(c);
     if (!ctx || !x || !w_q || !scales || !biases || !out) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
     if (act < LUX_QMM_ACT_NONE || act > LUX_QMM_ACT_GELU) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
-    if (M < 0) return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
-    LuxBackendError e = check_format(K, N, group_size, bits);
+    LuxBackendError e = lux_hip_qmm_validate(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype, kernel);
     if (e != LUX_BACKEND_OK) return e;
-    if (!dtype_ok(x_dtype) || !dtype_ok(sb_dtype) || !dtype_ok(out_dtype) || (bias && !dtype_ok(bias_dtype)))
-        return LUX_BACKEND_ERROR_NOT_SUPPORTED;
-    if (kernel != LUX_QMM_KERNEL_AUTO && kernel != LUX_QMM_KERNEL_GEMV && kernel != LUX_QMM_KERNEL_GEMM)
-        return LUX_BACKEND_ERROR_INVALID_ARGUMENT;
+    if (bias && !dtype_ok(bias_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
     const size_t G = (size_t)(K / group_size);
     if (!fits(B(x), (size_t)M * K * dtype_size(x_dtype)) ||
         !fits(B(w_q), (size_t)N * K * bits / 8) || !fits(B(scales), (size_t)N * G * dtype_size(sb_dtype)) ||
@@ -336,21 +386,11 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     a.bias = bias ? B(bias)->ptr : nullptr;
     a.bias_dtype = bias_dtype;
     a.act = act;
+    a.ws = ctx->ws;
+    a.ws_bytes = ctx->ws_bytes;
 
     if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
-    if (kernel == LUX_QMM_KERNEL_AUTO)
-        kernel = select_kernel_impl(M, K, N, group_size, bits, x_dtype, sb_dtype);
-    if (kernel == LUX_QMM_KERNEL_GEMM) {
-        // an explicit GEMM request runs the GEMM or fails: its numerics
-        // (weights rounded to the activation type) differ from the GEMV's
-        if (!gemm_ok(M, K, N, group_size, bits, x_dtype, sb_dtype)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
-        return map_status(lxq::launch_qgemm(a, ctx->stream));
-    }
-    if (K % 64 == 0) {
-        lxq::LuxStatus s = lxq::launch_qgemv(a, ctx->stream);
-        if (s != lxq::LuxStatus::NotSupported) return map_status(s);
-    }
-    return map_status(lxq::launch_qmm_generic(a, ctx->stream));
+    return lux_hip_qmm_dispatch(a, kernel, ctx->stream);
 }
 
 LuxBackendError hip_op_quantized_matmul(LuxBackendContext* c, LuxBackendBuffer* x,

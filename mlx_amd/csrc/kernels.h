@@ -38,6 +38,10 @@ struct QmmArgs {
     const void* bias = nullptr;  // fused epilogue: per-column bias [N] (bias_dtype) or none
     int bias_dtype = 0;
     int act = ACT_NONE;
+    // device workspace a kernel may use for partial sums and counters
+    // (counters zero between launches); null/0: kernels that need one are skipped
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
     Epilogue epi() const { return Epilogue{bias, bias_dtype, act, out_dtype}; }
     // kernels are instantiated with and without the output stage: the plain
     // op runs code with no bias or activation path at all
@@ -58,6 +62,19 @@ LuxStatus launch_qgemv_mid(const QmmArgs& a, hipStream_t st);
 // small-M MFMA GEMM (8 < M <= 64, f16/bf16 x, K % 1024 == 0); NotSupported
 // otherwise (launch_qgemm tries it first)
 LuxStatus launch_qgemm_small(const QmmArgs& a, hipStream_t st);
+// split-K small-M MFMA GEMM (8 < M <= 64, f16/bf16 x, K % 128 == 0): x read
+// once per 128 columns, the K parts summed through a.ws; NotSupported where
+// it does not apply or the workspace is too small (tried before the above)
+LuxStatus launch_qgemm_sk(const QmmArgs& a, hipStream_t st);
+// workspace bytes launch_qgemm_sk uses for this shape given `cap` bytes
+// (0: it needs none or does not apply)
+size_t qgemm_sk_workspace(int M, int K, int N, int bits, int x_dtype, size_t cap);
+// the workspace every caller of the split-K GEMM provides (a context's, or
+// the allocation-free entry point's static one): the same size everywhere,
+// so the same shape takes the same split, and the same result bits
+// (16 MiB of partials for the largest split, 512 blocks of 32 KiB, and the
+// tile counters)
+constexpr size_t kSplitWorkspaceBytes = (16u << 20) + 4096;
 // MFMA GEMM for f16/bf16 activations; needs K % 64 == 0
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st);
 // generic one-thread-per-output kernel for shapes the tiled kernels reject

@@ -5,9 +5,11 @@
 namespace lxq {
 
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st) {
-    // 8 < M <= 64: the W-streaming small-M kernel where it applies
+    // 8 < M <= 64: the split-K small-M kernel, else the W-streaming one
     if (a.M <= 64) {
-        const LuxStatus s = launch_qgemm_small(a, st);
+        LuxStatus s = launch_qgemm_sk(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+        s = launch_qgemm_small(a, st);
         if (s != LuxStatus::NotSupported) return s;
     }
     // the scale windows cover 4 K steps of 64 codes

@@ -1,0 +1,8 @@
+// qgemm_sk_b4.hip -- 4-bit instantiations of the split-K small-M GEMM.
+#include "qgemm_sk.h"
+
+namespace lxq {
+namespace sk {
+template LuxStatus launch_bits<4>(const QmmArgs&, int, hipStream_t);
+}  // namespace sk
+}  // namespace lxq

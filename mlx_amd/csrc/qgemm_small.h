@@ -86,7 +86,12 @@ template <int BITS, int TX>
 __device__ __forceinline__ u4 w_operand(const uint32_t* c, float sc, float bi, int s) {
     float q[8];
     if constexpr (BITS == 4) {
-        const uint32_t w = c[s], lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        uint32_t w = c[s], lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        // the nibble planes as opaque values: otherwise the compiler folds
+        // each mask into a bit-field extract per code, and then converts
+        // byte 0 of it (2 instructions per code instead of the 1 of
+        // v_cvt_f32_ubyte{0..3} on the plane)
+        asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             q[2 * e] = (float)((lo >> (8 * e)) & 0xffu);

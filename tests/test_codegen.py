@@ -21,6 +21,7 @@ import pytest
 LLVM = "/opt/rocm/llvm/bin"
 KERNELS = ("qgemv_stream_kernel", "qgemv_split_kernel", "qgemv_dec_kernel", "qmm_skinny_kernel")
 LINE = "qgemv_line_kernel"
+SK = "qgemm_sk_kernel"
 
 
 def _tool(name):
@@ -44,7 +45,7 @@ def disassembly(tmp_path_factory):
     for co in sorted(d.glob("plugin.so.*gfx950*")):
         syms = subprocess.run([objdump, "-t", str(co)], check=True, capture_output=True, text=True).stdout
         names = [ln.split()[-1] for ln in syms.splitlines()
-                 if " .text" in ln and any(k in ln for k in KERNELS + (LINE,)) and not ln.endswith(".kd")]
+                 if " .text" in ln and any(k in ln for k in KERNELS + (LINE, SK)) and not ln.endswith(".kd")]
         if not names:
             continue
         dis = subprocess.run([objdump, "-d", "--mcpu=gfx950", "--disassemble-symbols=" + ",".join(names), str(co)],
@@ -64,7 +65,7 @@ def test_weight_loads_precede_their_wait(disassembly):
     found = {k: 0 for k in KERNELS}
     bad = []
     for name, lines in disassembly.items():
-        if LINE in name:
+        if LINE in name or SK in name:
             continue
         loads, vm = 0, None
         for t in lines:
@@ -112,4 +113,31 @@ def test_line_kernel_issue_order(disassembly):
         if not any(t.startswith("buffer_load") and re.search(r"\bnt\b", t) for t in after[:wait]):
             bad.append(f"{name}: no code load between the barrier and the first wait")
     assert seen, "qgemv_line_kernel not found in the plugin"
+    assert not bad, "\n".join(bad[:10])
+
+
+def test_split_k_gemm_keeps_loads_in_flight(disassembly):
+    """The split-K small-M GEMM: (1) no L2 writeback or invalidate anywhere
+    (its partial sums cross XCDs through device-scope cache-policy loads and
+    stores; a device-scope fence there made launches 4-5x slower); (2) in the
+    main loop (the super-steps between the prologue's barrier and the fourth
+    after it) every wait leaves at least 8 vector-memory loads in flight: a
+    load the compiler cannot count (one issued on only some paths) makes it
+    drain them all before every super-step."""
+    seen, bad = 0, []
+    for name, lines in disassembly.items():
+        if SK not in name:
+            continue
+        seen += 1
+        if any(t.startswith(("buffer_wbl2", "buffer_inv")) for t in lines):
+            bad.append(f"{name}: L2 writeback/invalidate")
+        bars = [i for i, t in enumerate(lines) if t.startswith("s_barrier")]
+        if len(bars) < 5:
+            bad.append(f"{name}: {len(bars)} barriers")
+            continue
+        low = [int(m.group(1)) for t in lines[bars[0]:bars[4]]
+               for m in [re.search(r"s_waitcnt\b.*\bvmcnt\((\d+)\)", t)] if m and int(m.group(1)) < 8]
+        if low:
+            bad.append(f"{name}: main-loop waits down to vmcnt({min(low)})")
+    assert seen, "qgemm_sk_kernel not found in the plugin"
     assert not bad, "\n".join(bad[:10])

@@ -365,6 +365,51 @@ def test_small_gemm_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"small gemm b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_split_k_gemm_parity(ctx, oracle, bits, xd, sbd, od):
+    """8 < M <= 64 with K % 128 == 0 and K % 1024 != 0: the split-K small-M
+    GEMM, the GEMM form ("dequantize to T, then matmul").  The shapes take
+    the K-part counts 1 (3 super-steps), 3 (of 9), 15 (of 30), 10 (of 20)
+    and 31 (of 62), one and two M tiles, ragged M and N; the parts meet
+    through the context's workspace."""
+    O = oracle
+    for (M, K, N, gs) in [(9, 384, 77, 32), (12, 1152, 200, 64), (40, 3840, 300, 128),
+                          (64, 2560, 1000, 32), (17, 7936, 129, 64)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 31 + M)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, w_round=xd)
+        check_output(O, y, want, od, f"split-K gemm b{bits} M{M} K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("M,xd,sbd,od", [(33, F16, F16, F16), (64, BF16, BF16, F32), (16, BF16, F32, BF16)])
+def test_unsplit_wide_gemm_parity(ctx, oracle, M, xd, sbd, od):
+    """Wide N (>= 192 tiles of 128 columns) runs the same kernel unsplit,
+    with no workspace: 193 tiles, the last one ragged (N = 24600)."""
+    O = oracle
+    K, N, gs, bits = 1024, 24600, 64, 4
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=610 + M)
+    y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, variant="omp", w_round=xd)
+    check_output(O, y, want, od, f"unsplit wide M{M}")
+
+
+def test_split_k_shapes_in_sequence(ctx, oracle):
+    """Split-K GEMM launches of different shapes back to back on one
+    context workspace: a shape with few tiles and large partials (8 tiles,
+    14 K parts), then one with 188 tiles (2 K parts), then the first again.
+    Every tile counter must read zero at the start of each launch, so no
+    shape's partials may land on another's counter slots."""
+    O = oracle
+    A = (64, 3584, 1024, 4, 64)
+    B = (64, 2560, 24000, 4, 64)
+    for i, (M, K, N, bits, gs) in enumerate([A, B, A]):
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, BF16, BF16, seed=900 + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, BF16, BF16, F32, KERNELS["gemm"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, BF16, BF16, F32, variant="omp", w_round=BF16)
+        check_output(O, y, want, F32, f"split-K sequence launch {i} N={N}")
+
+
 @pytest.mark.parametrize("M,K,N,bits,gs,xd,kern", [
     (32, 8192, 8192, 8, 128, BF16, "gemm"),   # small-M GEMM, one block per CU
     (64, 4096, 11008, 3, 64, F16, "gemm"),    # two M tiles, ragged grid
@@ -462,6 +507,7 @@ FUSED_CASES = [
     (4, 4096, 64, 4, 64, BF16),     # decode MFMA kernel
     (6, 2048, 40, 8, 128, F16),     # mid-M ring kernel (8-bit)
     (32, 2048, 72, 4, 64, BF16),    # small-M GEMM
+    (40, 2560, 200, 4, 64, F16),    # split-K small-M GEMM (10 K parts)
     (96, 512, 136, 4, 64, F16),     # large GEMM
     (3, 96, 20, 4, 32, F32),        # generic kernel (K % 64 != 0)
 ]
@@ -530,6 +576,7 @@ def test_fused_errors(ctx, oracle):
 @pytest.mark.parametrize("M,K,N,bits,gs,xd,sbd,kern", [
     (96, 512, 136, 4, 64, BF16, BF16, "gemm"),   # large GEMM
     (32, 1024, 70, 3, 32, F16, F32, "gemm"),     # small-M GEMM
+    (24, 1152, 300, 4, 64, BF16, BF16, "gemm"),  # split-K small-M GEMM (3 K parts)
     (1, 4096, 96, 4, 64, F16, F16, "gemv"),      # whole-line GEMV
     (1, 14336, 40, 4, 64, F16, F16, "gemv"),     # split-K GEMV
     (2, 2048, 48, 8, 64, BF16, BF16, "gemv"),    # stream GEMV
