@@ -192,6 +192,27 @@ typedef bool (*lux_gpu_backend_quant_init_fn)(const lux_gpu_quant_vtbl** out);
  */
 __attribute__((visibility("default"))) bool lux_gpu_backend_quant_init(const lux_gpu_quant_vtbl** out);
 
+/*
+ * op_quantized_matmul_ex without a context and without allocation: no
+ * counterpart in the reference.  It is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  x, w_q, scales, biases and out are device pointers of the
+ * current device holding at least the bytes the shape needs (not checked:
+ * there are no buffer sizes here); `stream` is a hipStream_t of that device
+ * (NULL: the null stream).  Same kernels, selection, results and shape and
+ * dtype errors as op_quantized_matmul_ex.  The split-K small-M GEMM's
+ * partial sums and tile counters live in a 16 MiB static device array that
+ * each GPU holds until the process ends (shapes whose split would need more
+ * are INVALID_ARGUMENT; the split rule keeps every shape within it).  All
+ * calls on one GPU share that array: calls that overlap in time on one GPU
+ * (concurrent streams, or threads) race and give wrong results.  The first
+ * call on a device clears the array with a kernel on its stream.
+ */
+__attribute__((visibility("default"))) LuxBackendError lux_gpu_quantized_matmul_noalloc(
+    const void* x, const void* w_q, const void* scales, const void* biases, void* out, int M, int K, int N,
+    int group_size, int bits, LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype, LuxBackendDtype out_dtype,
+    LuxQuantKernel kernel, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

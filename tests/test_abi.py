@@ -75,7 +75,7 @@ def test_plugin_exports_exactly_the_declared_symbols():
     out = _run(["nm", "-D", "--defined-only", mlx_amd.PLUGIN_PATH])
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     declared = declared_symbols()
-    assert declared == {"lux_gpu_backend_init", "lux_gpu_backend_quant_init"}
+    assert declared == {"lux_gpu_backend_init", "lux_gpu_backend_quant_init", "lux_gpu_quantized_matmul_noalloc"}
     assert declared <= exported
     # nothing else leaks from the plugin (hidden visibility)
     assert {s for s in exported if s.startswith("lux")} == declared

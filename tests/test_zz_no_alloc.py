@@ -1,0 +1,104 @@
+"""The allocation-free entry point lux_gpu_quantized_matmul_noalloc, called
+through the C ABI on raw device pointers and a caller stream, against the
+context op op_quantized_matmul_ex on the same inputs: bit for bit (the same
+kernels, and the same K split, since its static scratch is the size of a
+context's workspace), and within the output gate of the oracle.  Two calls
+in a row share the scratch, the second with a smaller input; the large one
+runs the split-K GEMM with its parts meeting in the scratch, so a counter
+left nonzero by the first call would break the second.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from qmm_util import BF16, F16, F32, check_output
+
+pytestmark = pytest.mark.gpu
+
+# (M, K, N, bits, group size, x dtype, scales dtype, out dtype, kernel)
+CALLS = [
+    (64, 3584, 4096, 3, 64, F16, F16, F16, 0),     # split-K GEMM, 7 K parts, 224 blocks
+    (17, 1152, 200, 4, 32, BF16, BF16, F32, 2),    # split-K GEMM, 3 K parts, 6 blocks
+    (1, 4096, 512, 4, 64, F16, F16, F16, 0),       # a GEMV: no scratch
+]
+
+
+class _Hip:
+    def __init__(self):
+        self.L = ctypes.CDLL("libamdhip64.so", mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+
+    def ck(self, rc, what):
+        assert rc == 0, f"{what}: hipError {rc}"
+
+    def upload(self, a):
+        p = ctypes.c_void_p()
+        self.ck(self.L.hipMalloc(ctypes.byref(p), ctypes.c_size_t(max(1, a.nbytes))), "hipMalloc")
+        self.ck(self.L.hipMemcpy(p, a.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(a.nbytes), 1), "hipMemcpy")
+        return p
+
+    def alloc(self, n):
+        p = ctypes.c_void_p()
+        self.ck(self.L.hipMalloc(ctypes.byref(p), ctypes.c_size_t(n)), "hipMalloc")
+        self.ck(self.L.hipMemset(p, 0xFF, ctypes.c_size_t(n)), "hipMemset")
+        return p
+
+    def download(self, p, dtype, shape):
+        a = np.empty(shape, dtype)
+        self.ck(self.L.hipMemcpy(a.ctypes.data_as(ctypes.c_void_p), p, ctypes.c_size_t(a.nbytes), 2), "hipMemcpy")
+        return a
+
+    def free(self, p):
+        self.ck(self.L.hipFree(p), "hipFree")
+
+
+def _entry():
+    import mlx_amd
+    lib = ctypes.CDLL(mlx_amd.PLUGIN_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    f = lib.lux_gpu_quantized_matmul_noalloc
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 8 + [ctypes.c_int, ctypes.c_void_p]
+    return f
+
+
+def test_noalloc_matches_context_op(ctx, oracle):
+    from mlx_amd import runtime
+    O = oracle
+    f = _entry()
+    hip = _Hip()
+    stream = ctypes.c_void_p()
+    hip.ck(hip.L.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    try:
+        for i, (M, K, N, bits, gs, xd, sbd, od, kern) in enumerate(CALLS):
+            print(f"[case] noalloc call {i}: M={M} K={K} N={N} b={bits} g={gs} x={xd} kernel={kern}", flush=True)
+            x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=700 + i)
+            ptrs = [hip.upload(np.ascontiguousarray(a)) for a in (x, w_q, s, b)]
+            nbytes = M * N * runtime.esize(od)
+            out = hip.alloc(nbytes)
+            try:
+                rc = f(*ptrs, out, M, K, N, gs, bits, xd, sbd, od, kern, stream)
+                assert rc == 0, f"noalloc returned {rc}"
+                hip.ck(hip.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
+                got = hip.download(out, runtime.np_dtype(od), (M, N))
+            finally:
+                for p in ptrs + [out]:
+                    hip.free(p)
+            want = runtime.run_quantized_matmul(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, kern)
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"call {i} differs from the context op"
+            gemm = ctx.select_kernel(M, K, N, gs, bits, xd, sbd) == 2 if kern == 0 else kern == 2
+            ref = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, variant="omp",
+                                     w_round=xd if gemm else F32)
+            check_output(O, got, ref, od, f"noalloc call {i}")
+    finally:
+        hip.ck(hip.L.hipStreamDestroy(stream), "hipStreamDestroy")
+
+
+def test_noalloc_errors():
+    """Errors come back before any device work: null pointers, a bad shape."""
+    f = _entry()
+    p = ctypes.c_void_p(16)
+    assert f(None, p, p, p, p, 16, 256, 8, 64, 4, F16, F16, F16, 0, None) == 1  # INVALID_ARGUMENT
+    assert f(p, p, p, p, p, 16, 100, 8, 64, 4, F16, F16, F16, 0, None) == 1     # K % group size
+    assert f(p, p, p, p, p, 16, 256, 8, 64, 7, F16, F16, F16, 0, None) != 0     # bits outside the format
+    assert f(p, p, p, p, p, 16, 256, 8, 64, 4, F16, F16, F16, 9, None) == 1     # unknown kernel
