@@ -21,6 +21,15 @@ static LuxStatus launch_bits(const QmmArgs& a, hipStream_t st) {
     }
 }
 
+static LuxStatus launch_mx_bits(const QmmArgs& a, hipStream_t st) {
+    switch (a.bits) {
+    case 2: return launch_mx_b<2>(a, st);
+    case 4: return launch_mx_b<4>(a, st);
+    case 8: return launch_mx_b<8>(a, st);
+    default: return LuxStatus::NotSupported;
+    }
+}
+
 // M is processed in chunks of up to 8 rows of x, as many as the staged x
 // fits in 64 KB of LDS (two blocks per CU).
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
@@ -39,6 +48,13 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     //    (K = 14336, N = 4096: 18.1 us against 25.7 on the LDS-ring kernel;
     //    8-bit K = 12288: 17.7 against 25.3); at K <= 8192 the decode kernel
     //    is faster (K = 8192, N = 8192: 12.8 against 18.1).
+    // 2..4 rows of x with K <= 4096: the K-split whole-line kernel where it
+    // applies and measured faster (qgemv_mx.h: 8-bit codes, 2-bit at M >= 3,
+    // 4-bit at M = 2 with f16 x)
+    if (args.M >= 2 && args.M <= 4) {
+        const LuxStatus s = launch_mx_bits(args, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     const bool stream2 = args.M == 2 && args.x_dtype != DT_F32 && (args.K <= 4096 || (args.K > 8192 && args.K <= 16384));
     const bool ring8 = !(args.bits == 8 && args.M <= 8 && args.K <= 4096);
     if (args.M >= 2 && args.M <= 8 && !stream2) {

@@ -930,6 +930,12 @@ LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
 template <int BITS, int TX>
 LuxStatus launch_line(const QmmArgs& a, hipStream_t st);
 
+// 2 <= M <= 4, K <= 4096: the K-split whole-line kernel of qgemv_mx.h
+// (defined there, instantiated by the per-bit-width translation units);
+// NotSupported for shapes it does not take
+template <int BITS>
+LuxStatus launch_mx_b(const QmmArgs& a, hipStream_t st);
+
 template <int BITS, int TX>
 LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
     if (a.M == 1 && a.K <= 4096) {

@@ -52,19 +52,19 @@ struct LineCfg {
 typedef uint32_t v3u32 __attribute__((ext_vector_type(3)));
 constexpr int kCachePolicyNT = 2;  // buffer-load cache policy bit: non-temporal
 
-// x operands of one chunk
-template <int BITS, int TX, int OP>
+// x operands of one chunk of NC_ codes (default: the whole-line chunk)
+template <int BITS, int TX, int OP, int NC_ = LineCfg<BITS>::NC>
 struct LineX {
-    static constexpr int NC = LineCfg<BITS>::NC;
+    static constexpr int NC = NC_;
     static constexpr int kRegs = OP == OP_F32 ? NC : NC / 2;
     uint32_t v[kRegs];
     float h0, h1;  // sums of x over the chunk's two halves (times 2^-24 for the subnormal forms)
 };
 
 // nat: the chunk's x values in natural order (NC elements)
-template <int BITS, int TX, int OP>
-__device__ __forceinline__ void prep_line_x(const uint32_t* nat, LineX<BITS, TX, OP>& o) {
-    constexpr int NC = LineCfg<BITS>::NC;
+template <int BITS, int TX, int OP, int NC_ = LineCfg<BITS>::NC>
+__device__ __forceinline__ void prep_line_x(const uint32_t* nat, LineX<BITS, TX, OP, NC_>& o) {
+    constexpr int NC = NC_;
     if constexpr (OP == OP_F32) {
         float a = 0.f, b = 0.f;
 #pragma unroll
@@ -131,10 +131,11 @@ __device__ __forceinline__ void prep_line_x(const uint32_t* nat, LineX<BITS, TX,
 
 // partial of one chunk for one row.  TWO: s0/b0 cover the chunk's first half
 // and s1/b1 its second (2-bit codes, group size 32); otherwise s1/b1 unused.
-template <int BITS, int TX, int OP, bool TWO>
-__device__ __forceinline__ float line_partial(const uint32_t* w, const LineX<BITS, TX, OP>& xo, float s0, float b0,
+// w: the chunk's NC_ * BITS / 32 code words.
+template <int BITS, int TX, int OP, bool TWO, int NC_ = LineCfg<BITS>::NC>
+__device__ __forceinline__ float line_partial(const uint32_t* w, const LineX<BITS, TX, OP, NC_>& xo, float s0, float b0,
                                               float s1, float b1) {
-    constexpr int NC = LineCfg<BITS>::NC, WPI = LineCfg<BITS>::WPI;
+    constexpr int NC = NC_, WPI = NC_ * BITS / 32;
     if constexpr (OP == OP_SUB4) {
         float a = 0.f, c = 0.f;
 #pragma unroll

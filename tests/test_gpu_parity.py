@@ -148,6 +148,28 @@ def test_split_k_full(ctx, oracle, K, N, xd):
     check_output(O, y, want, xd, f"split-K full K{K} N{N}")
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_kline_gemv_parity(ctx, oracle, bits, xd, sbd, od):
+    """2 <= M <= 4 rows of x with K <= 4096 (K % 256 == 0, each quarter of K
+    a whole number of groups) runs the K-split whole-line kernel where it is
+    the faster one: 8-bit codes at M = 2..4, 2-bit at M = 3 and 4, 4-bit at
+    M = 2 with f16 x (the other cases check the kernels that take them).
+    M = 3 carries a fourth x row that is never stored; 16- and 28-row blocks
+    (N = 7150: 256 blocks of 28, the last ragged); a quarter of K narrower
+    than a wave (K = 256: 4 of 64 lanes hold codes); every group size."""
+    O = oracle
+    Ms = {2: (3, 4), 4: (2,), 8: (2, 3, 4)}[bits]
+    shapes = [(Ms[i % len(Ms)], K, N, gs) for i, (K, N, gs) in
+              enumerate([(4096, 300, 64), (1024, 77, 32), (2048, 129, 128), (256, 40, 64), (512, 57, 128),
+                         (4096, 7150, 32)])]
+    for (M, K, N, gs) in shapes:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 41 + M + K)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"k-line b{bits} M{M} K{K} N{N} g{gs}")
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
@@ -173,13 +195,13 @@ def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
                                        (F16, BF16, F32), (BF16, F32, BF16)])
 def test_decode_mfma_parity(ctx, oracle, xd, sbd, od):
     """2 <= M <= 8 with 4-bit codes and K % 1024 == 0 runs the MFMA decode
-    kernel (M = 2 only for K > 4096): every group size (all three lane
-    regroupings), one to eight K waves, N not a multiple of the 32-row block,
-    M at both ends.  f32 scales with group size 32 fall back to the LDS-ring
-    kernel."""
+    kernel (M <= 4 only for K > 4096, M = 2 only for 4096 < K <= 8192):
+    every group size (all three lane regroupings), one to eight K waves, N
+    not a multiple of the 32-row block, M at both ends.  f32 scales with
+    group size 32 fall back to the LDS-ring kernel."""
     O = oracle
-    for (M, K, N, gs) in [(2, 6144, 45, 64), (8, 4096, 100, 64), (3, 2048, 77, 32), (7, 8192, 33, 128),
-                          (4, 4096, 64, 32), (6, 3072, 19, 128), (5, 1024, 128, 64), (8, 8192, 50, 32)]:
+    for (M, K, N, gs) in [(2, 6144, 45, 64), (8, 4096, 100, 64), (3, 8192, 77, 32), (7, 8192, 33, 128),
+                          (4, 5120, 64, 32), (6, 3072, 19, 128), (5, 1024, 128, 64), (8, 8192, 50, 32)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, 4, gs, xd, sbd, seed=11 * M + gs)
         y = run(ctx, x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od, KERNELS["gemv"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od)
@@ -501,10 +523,12 @@ FUSED_CASES = [
     # M, K, N, bits, gs, x dtype: AUTO routes each to a different kernel
     (1, 4096, 300, 4, 64, F16),     # whole-line GEMV
     (1, 14336, 70, 4, 64, BF16),    # split-K GEMV
-    (2, 4096, 40, 4, 64, F16),      # stream GEMV (two rows of x)
+    (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
+    (2, 4096, 40, 3, 64, F16),      # stream GEMV (two rows of x, 3-bit)
     (6, 960, 70, 3, 64, F16),       # row-run GEMV (3-bit, K % 1024 != 0)
     (6, 512, 96, 4, 64, BF16),      # skinny MFMA GEMV
-    (4, 4096, 64, 4, 64, BF16),     # decode MFMA kernel
+    (3, 1024, 72, 8, 128, BF16),    # K-split whole-line GEMV (three rows of x, 8-bit)
+    (6, 4096, 64, 4, 64, BF16),     # decode MFMA kernel
     (6, 2048, 40, 8, 128, F16),     # mid-M ring kernel (8-bit)
     (32, 2048, 72, 4, 64, BF16),    # small-M GEMM
     (40, 2560, 200, 4, 64, F16),    # split-K small-M GEMM (10 K parts)
@@ -579,8 +603,9 @@ def test_fused_errors(ctx, oracle):
     (24, 1152, 300, 4, 64, BF16, BF16, "gemm"),  # split-K small-M GEMM (3 K parts)
     (1, 4096, 96, 4, 64, F16, F16, "gemv"),      # whole-line GEMV
     (1, 14336, 40, 4, 64, F16, F16, "gemv"),     # split-K GEMV
-    (2, 2048, 48, 8, 64, BF16, BF16, "gemv"),    # stream GEMV
-    (4, 4096, 64, 4, 64, BF16, BF16, "gemv"),    # decode MFMA kernel
+    (2, 2048, 48, 8, 64, BF16, BF16, "gemv"),    # K-split whole-line GEMV
+    (2, 2048, 48, 3, 64, F16, F16, "gemv"),      # stream GEMV
+    (6, 4096, 64, 4, 64, BF16, BF16, "gemv"),    # decode MFMA kernel
     (8, 1024, 40, 8, 128, F16, F16, "gemv"),     # mid-M ring kernel
     (3, 96, 20, 5, 32, F32, F32, "gemv"),        # generic kernel
 ])
