@@ -48,9 +48,10 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     //    (K = 14336, N = 4096: 18.1 us against 25.7 on the LDS-ring kernel;
     //    8-bit K = 12288: 17.7 against 25.3); at K <= 8192 the decode kernel
     //    is faster (K = 8192, N = 8192: 12.8 against 18.1).
-    // 2..4 rows of x with K <= 4096: the K-split whole-line kernel where it
-    // applies and measured faster (qgemv_mx.h: 8-bit codes, 2-bit at M >= 3,
-    // 4-bit at M = 2 with f16 x)
+    // 2..4 rows of x with K <= 16384: the K-split whole-line kernel where it
+    // applies and measured faster (qgemv_mx.h, mx_wins: every K > 8192; M = 2
+    // and 2-bit codes up to K = 8192; at K <= 4096 8-bit codes, 2-bit at
+    // M >= 3, 4-bit at M = 2 with f16 x)
     if (args.M >= 2 && args.M <= 4) {
         const LuxStatus s = launch_mx_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;

@@ -191,6 +191,24 @@ def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"small-M b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_kline_gemv_long_k(ctx, oracle, bits, xd, sbd, od):
+    """2 <= M <= 4 with 4096 < K <= 16384 (down projections): the K-split
+    whole-line kernel with 8 waves per block (4096 < K <= 8192, where it takes
+    M = 2 and 2-bit codes) and 16 (K <= 16384, every M), each wave's part
+    under a whole wave (K = 6144: 768 codes, 48 lanes), every group size, f32
+    scales whose block rows take two LDS passes (K = 16384, g32), ragged N."""
+    O = oracle
+    for i, (K, N, gs) in enumerate([(6144, 100, 64), (8192, 33, 32), (14336, 70, 32), (16384, 40, 128),
+                                    (16384, 18, 32), (12288, 50, 64)]):
+        M = (2 if bits != 2 else 3) if K <= 8192 else 2 + i % 3
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 43 + M + K)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"k-line long K b{bits} M{M} K{K} N{N} g{gs}")
+
+
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32),
                                        (F16, BF16, F32), (BF16, F32, BF16)])
 def test_decode_mfma_parity(ctx, oracle, xd, sbd, od):
