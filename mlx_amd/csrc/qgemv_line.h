@@ -7,7 +7,10 @@
 // A block is 4 waves, wave w owns R consecutive rows (R = 4 or 7, whichever
 // spreads the blocks more evenly over the 256 CUs).  Every load is issued
 // at the start, straight into registers:
-//   1. x: the lane's code chunks' x values (L2-resident after first touch);
+//   1. x: the lane's code chunks' x values (L2-resident after first touch),
+//      or, for the widths and types where it measured faster, the block's
+//      x once (16 bytes per thread), shared through LDS after the codes are
+//      issued;
 //   2. the wave's R scale rows and R bias rows, as whole 16-byte chunks;
 //   3. a block barrier, so that the x and scale requests of all four waves
 //      enter the CU's vector-memory queue ahead of every code request;
@@ -230,6 +233,7 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
     constexpr int XW = NC * XE / 4;  // 32-bit words of x per chunk
     constexpr int NT = TWO ? 2 : 1;  // groups per chunk
     static_assert(R == 4 || R == 7, "rows per wave");
+    static_assert(NI * 64 * NC <= 4096, "the lanes' chunks lie in the block's copy of x");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
@@ -243,17 +247,38 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
 #pragma unroll
     for (int i = 0; i < NI; i++) ok[i] = (uint32_t)(i * 64 + lane) * NC < (uint32_t)K;
 
-    // ---- 1. x of the lane's chunks ----
-    uint32_t xn[NI][XW];
+    // ---- 1. x.  XSH: once per block, thread t loading 16-byte chunks t,
+    // t + 256, ... of the 4096 codes' x (past K: zeros), shared through LDS
+    // (step 6); else each wave loads its lanes' chunks.  Measured (same box,
+    // stream launches, µs): shared x 4.80 against 5.21 at configs[0] (f32
+    // x), 6.95 against 7.12 at 2-bit, 8.90 against 9.09 at 6-bit, level at
+    // 3- and 8-bit, but 7.67 against 7.37-7.54 at configs[1] (4-bit, f16 x),
+    // where the block barrier before the x reads costs more than the queue
+    // time of the per-wave copies. ----
+    constexpr bool XSH = !(BITS == 4 && TX != DT_F32);
+    constexpr int kXQ = XSH ? 4096 * XE / 4096 : 1;  // 16-byte chunks per thread
+    const int tid = threadIdx.x;
+    uint32_t xq[kXQ][4];
+    uint32_t xw[XSH ? 1 : NI][XW];
     {
         const auto xr = buf_rsrc(x, (uint32_t)K * XE);
+        if constexpr (XSH) {
 #pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const uint32_t off = ok[i] ? (uint32_t)(i * 64 + lane) * NC * XE : kZeroOff;
+            for (int q = 0; q < kXQ; q++) {
+                const uint32_t c = (uint32_t)(q * 256 + tid);
+                const uint32_t off = c * 16u < (uint32_t)K * XE ? c * 16u : kZeroOff;
+                const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+                xq[q][0] = v.x; xq[q][1] = v.y; xq[q][2] = v.z; xq[q][3] = v.w;
+            }
+        } else {
 #pragma unroll
-            for (int j = 0; j < XW / 4; j++) {
-                const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * j, 0, 0);
-                xn[i][4 * j] = v.x; xn[i][4 * j + 1] = v.y; xn[i][4 * j + 2] = v.z; xn[i][4 * j + 3] = v.w;
+            for (int i = 0; i < NI; i++) {
+                const uint32_t off = ok[i] ? (uint32_t)(i * 64 + lane) * NC * XE : kZeroOff;
+#pragma unroll
+                for (int j = 0; j < XW / 4; j++) {
+                    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * j, 0, 0);
+                    xw[i][4 * j] = v.x; xw[i][4 * j + 1] = v.y; xw[i][4 * j + 2] = v.z; xw[i][4 * j + 3] = v.w;
+                }
             }
         }
     }
@@ -352,10 +377,32 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
         }
     }
 
-    // ---- 6. x operands (the first loads to land) ----
+    // ---- 6. x operands.  XSH: x into the block's LDS copy (the first
+    // loads to land: the wait leaves the codes in flight), a barrier, then
+    // each lane's chunks (chunks past K hold zeros: their partials are
+    // exactly 0); else the wave's own loads ----
     LineX<BITS, TX, OP> xo[NI];
+    if constexpr (XSH) {
+        __shared__ __attribute__((aligned(16))) uint8_t lx[4096 * XE];
 #pragma unroll
-    for (int i = 0; i < NI; i++) prep_line_x<BITS, TX, OP>(xn[i], xo[i]);
+        for (int q = 0; q < kXQ; q++)
+            *reinterpret_cast<v4u32*>(lx + (q * 256 + tid) * 16) = v4u32{xq[q][0], xq[q][1], xq[q][2], xq[q][3]};
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            uint32_t xn[XW];
+            const uint8_t* src = lx + (i * 64 + lane) * NC * XE;
+#pragma unroll
+            for (int j = 0; j < XW / 4; j++) {
+                const v4u32 v = *reinterpret_cast<const v4u32*>(src + 16 * j);
+                xn[4 * j] = v.x; xn[4 * j + 1] = v.y; xn[4 * j + 2] = v.z; xn[4 * j + 3] = v.w;
+            }
+            prep_line_x<BITS, TX, OP>(xn, xo[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NI; i++) prep_line_x<BITS, TX, OP>(xw[i], xo[i]);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 7. rows in arrival order ----
