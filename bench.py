@@ -408,12 +408,22 @@ SWEEP = [
 ]
 
 
-def sweep(ctx, hip, steps, only=None):
+def parse_shape(spec):
+    """'M,K,N,bits,group,x' (x: f16, bf16 or f32; scales and output in the
+    same type) -> a SWEEP-style tuple named 'shape'."""
+    f = spec.split(",")
+    if len(f) != 6:
+        raise SystemExit(f"--shape wants M,K,N,bits,group,x; got {spec!r}")
+    dt = {"f16": F16, "bf16": BF16, "f32": F32}[f[5]]
+    return ("shape", int(f[0]), int(f[1]), int(f[2]), int(f[3]), int(f[4]), dt, dt, dt)
+
+
+def sweep(ctx, hip, steps, only=None, table=SWEEP):
     """One line per config: kernel AUTO picks, per-launch time (stream and
     graph replays), weight GB/s and TFLOP/s with their roofline fractions."""
     from mlx_amd import abi
     names = {abi.KERNEL_GEMV: "gemv", abi.KERNEL_GEMM: "gemm"}
-    for name, M, K, N, bits, gs, xd, sbd, od in SWEEP:
+    for name, M, K, N, bits, gs, xd, sbd, od in table:
         if only and name not in only:
             continue
         kern = ctx.select_kernel(M, K, N, gs, bits, xd, sbd)
@@ -472,6 +482,8 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE config")
     ap.add_argument("--only", default="", help="with --sweep: comma-separated config names (c0..c4)")
+    ap.add_argument("--shape", action="append", default=[], metavar="M,K,N,BITS,GROUP,X",
+                    help="instead of the headline line, a sweep line for this shape (repeatable; for profiling)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the configs[1] M=4 and M=8 decode legs (for profiling)")
     ap.add_argument("--ceiling-only", action="store_true", help="only the ceiling leg (for profiling)")
@@ -495,6 +507,10 @@ def main():
     wb = weight_bytes(N, K, bits, gs, F16)
     if args.sweep:
         sweep(ctx, hip, min(args.steps, 256), [s for s in args.only.split(",") if s])
+        ctx.close()
+        return
+    if args.shape:
+        sweep(ctx, hip, min(args.steps, 256), None, [parse_shape(s) for s in args.shape])
         ctx.close()
         return
     if args.decode_only:

@@ -164,23 +164,29 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qgemm_sk_kernel(
     uint32_t cw[PD][CW];
     SbRaw<SB> sv[PD][NG], bv[PD][NG];
 
-    auto issue = [&](int slot, int u) {
+    // the same buffers with no records: every access is out of range and
+    // reads zeros without a memory request
+    const auto xr0 = rsrc(x, 0), wr0 = rsrc(wq, 0), sr0 = rsrc(scales, 0), br0 = rsrc(biases, 0);
+    auto issue = [&](int slot, int u, bool past) {
         // x tile, codes, scales and biases of super-step u into register
         // slot `slot`, as one batch in this order: the waits are counted in
-        // issue order, so the scheduler may not move loads across batches
+        // issue order, so the scheduler may not move loads across batches.
+        // `past` (uniform): a refill past the part's last super-step, issued
+        // all the same (see the prologue) but from the empty buffers
         __builtin_amdgcn_sched_barrier(0);
+        const auto xd = past ? xr0 : xr, wd = past ? wr0 : wr, sd = past ? sr0 : sr, bd = past ? br0 : br;
 #pragma unroll
         for (int i = 0; i < XR; i++) {
-            const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i] + (uint32_t)u * kSS * 2, 0, 0);
+            const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xd, xoff[i] + (uint32_t)u * kSS * 2, 0, 0);
             xv[slot][i][0] = v.x; xv[slot][i][1] = v.y; xv[slot][i][2] = v.z; xv[slot][i][3] = v.w;
         }
-        load_codes<BITS>(wr, woff + (uint32_t)u * kSS * BITS / 8, cw[slot]);
+        load_codes<BITS>(wd, woff + (uint32_t)u * kSS * BITS / 8, cw[slot]);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
             // group size 32: the second group of the half starts 32 codes later
             const uint32_t o = soff + ((uint32_t)u * kSS / GS + g) * kSb;
-            sv[slot][g] = load_sb<SB>(sr, o);
-            bv[slot][g] = load_sb<SB>(br, o);
+            sv[slot][g] = load_sb<SB>(sd, o);
+            bv[slot][g] = load_sb<SB>(bd, o);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -198,12 +204,12 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qgemm_sk_kernel(
         for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
 
     // Loads are issued unconditionally, past the part's last super-step too
-    // (they then re-read that super-step, L2-resident, into a slot nothing
-    // reads): a conditional issue leaves the compiler unable to count the
-    // loads in flight, and it then drains them all before every super-step.
+    // (from the empty buffers, into a slot nothing reads): a conditional
+    // issue leaves the compiler unable to count the loads in flight, and it
+    // then drains them all before every super-step.
     // ---- prologue: super-steps 0 .. PD-1 in flight, x(0) into buffer 0 ----
 #pragma unroll
-    for (int p = 0; p < PD; p++) issue(p, min(p, nss - 1));
+    for (int p = 0; p < PD; p++) issue(p, min(p, nss - 1), p >= nss);
     write_x(0, 0);
     lds_fence_barrier();
 
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qgemm_sk_kernel(
             if (u + 1 < nss) write_x((jj + 1) % PD, (u + 1) & 1);
             compute(jj, u);
             // refill this register slot with super-step u + PD
-            issue(jj, min(u + PD, nss - 1));
+            issue(jj, min(u + PD, nss - 1), u + PD >= nss);
             lds_fence_barrier();
         }
     }
@@ -315,27 +321,40 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qgemm_sk_kernel(
     // the last part of this tile: add the S partials in part order, store y,
     // and zero the counter again for the next launch
     if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // parts in order (the same order whichever block is last), each part's
-    // row groups loaded together
+    // parts in order (the same order whichever block is last); up to kPB
+    // parts' row groups are loaded together, one memory round trip per kPB
+    // parts (one part per trip left S round trips at the kernel's tail:
+    // 7 parts, K = 3584, took 21 µs)
+    constexpr int kPB = 4;
     float sum[MT][4][4];
-    for (int q_part = 0; q_part < S; q_part++) {
-        u4 v[MT][4];
+    for (int q0 = 0; q0 < S; q0 += kPB) {
+        u4 v[kPB][MT][4];
+        // loads on every path (parts past S re-read part S - 1, row groups
+        // past M their never-written slots; neither is used): a load on only
+        // some paths makes the compiler drain the ones before it
 #pragma unroll
-        for (int t = 0; t < MT; t++)
+        for (int pp = 0; pp < kPB; pp++) {
+            const int qp = q0 + pp < S ? q0 + pp : S - 1;
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (32 * t + 8 * q < M)
-                    v[t][q] = __builtin_amdgcn_raw_buffer_load_b128(pr, part_off(q_part, t, q), 0, kCachePolicyDevice);
+            for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int t = 0; t < MT; t++)
+                for (int q = 0; q < 4; q++)
+                    v[pp][t][q] = __builtin_amdgcn_raw_buffer_load_b128(pr, part_off(qp, t, q), 0, kCachePolicyDevice);
+        }
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (32 * t + 8 * q < M) {
-                    const float f[4] = {__uint_as_float(v[t][q].x), __uint_as_float(v[t][q].y),
-                                        __uint_as_float(v[t][q].z), __uint_as_float(v[t][q].w)};
+        for (int pp = 0; pp < kPB; pp++)
+            if (q0 + pp < S)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) sum[t][q][e] = q_part == 0 ? f[e] : sum[t][q][e] + f[e];
-                }
+                for (int t = 0; t < MT; t++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        if (32 * t + 8 * q < M) {
+                            const float f[4] = {__uint_as_float(v[pp][t][q].x), __uint_as_float(v[pp][t][q].y),
+                                                __uint_as_float(v[pp][t][q].z), __uint_as_float(v[pp][t][q].w)};
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                sum[t][q][e] = q0 + pp == 0 ? f[e] : sum[t][q][e] + f[e];
+                        }
     }
 #pragma unroll
     for (int t = 0; t < MT; t++)

@@ -77,7 +77,8 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const LuxStatus s = launch_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
-    int chunk = 8;
+    // (f32 x: at most 4 rows, the row-run kernel's registers at 8 do not fit)
+    int chunk = args.x_dtype == DT_F32 ? 4 : 8;
     while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
     // one row of x may still run on the split-K stream kernel (K <= 32768),
     // which stages x in up to 160 KB; the row-run kernel declines it itself

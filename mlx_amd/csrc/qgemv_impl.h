@@ -818,7 +818,16 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
                 b1 = SB == DT_F16 ? f16_to_f32(pb[1]) : bf16_to_f32(pb[1]);
             }
         }
-        if (!active) s0 = b0 = s1 = b1 = 0.f;
+        {
+            // idle lanes: scales zeroed by a mask, not a branch (with a
+            // branch per row at group size 32 the compiler kept every row's
+            // decoded codes live at once and spilled them to scratch)
+            const uint32_t am = active ? ~0u : 0u;
+            s0 = __uint_as_float(__float_as_uint(s0) & am);
+            b0 = __uint_as_float(__float_as_uint(b0) & am);
+            s1 = __uint_as_float(__float_as_uint(s1) & am);
+            b1 = __uint_as_float(__float_as_uint(b1) & am);
+        }
 #pragma unroll
         for (int m = 0; m < MR; m++) acc[r * MR + m] = row_partial<BITS, TX, OP, TWO>(w[r], xo[m], s0, b0, s1, b1);
     }
@@ -962,7 +971,10 @@ LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
     if (a.M <= 1) return launch_t<BITS, TX, 1>(a, st);
     if (a.M <= 2) return launch_t<BITS, TX, 2>(a, st);
     if (a.M <= 4) return launch_t<BITS, TX, 4>(a, st);
-    return launch_t<BITS, TX, 8>(a, st);
+    // f32 x comes in chunks of at most 4 rows: 8 rows of f32 x spilled
+    // 500-700 VGPRs to scratch
+    if constexpr (TX == DT_F32) return LuxStatus::NotSupported;
+    else return launch_t<BITS, TX, 8>(a, st);
 }
 
 template <int BITS>

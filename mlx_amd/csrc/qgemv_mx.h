@@ -261,11 +261,13 @@ LuxStatus launch_mx_q(const QmmArgs& a, hipStream_t st) {
     }
 }
 
-// waves per block: each covers at most 1024 codes of K; 8 and 16 waves
-// (2 and 4 waves per SIMD) take 16-row blocks, whose registers fit 128
+// waves per block: each covers at most 1024 codes of K; 8 waves (2 per
+// SIMD, 256 VGPRs) take 16-row blocks, 16 waves (4 per SIMD, 128 VGPRs) 16
+// rows of codes up to 4 bits and 8 rows of 8-bit codes (16 rows of 8-bit
+// codes are 64 VGPRs of code words alone and spilled to scratch)
 template <int BITS, int TX, int SB, int MX>
 LuxStatus launch_mx_r(const QmmArgs& a, hipStream_t st) {
-    if (a.K > 8192) return launch_mx_q<BITS, TX, SB, MX, 16, 16>(a, st);
+    if (a.K > 8192) return launch_mx_q<BITS, TX, SB, MX, BITS == 8 ? 8 : 16, 16>(a, st);
     if (a.K > 4096) return launch_mx_q<BITS, TX, SB, MX, 16, 8>(a, st);
     return mx_rows(a.N) == 28 ? launch_mx_q<BITS, TX, SB, MX, 28, 4>(a, st) : launch_mx_q<BITS, TX, SB, MX, 16, 4>(a, st);
 }
@@ -289,7 +291,7 @@ LuxStatus launch_mx_m(const QmmArgs& a, hipStream_t st) {
 //  * K > 8192 (down projections, where the decode kernel stops and the
 //    LDS-ring kernel took M >= 3): K = 14336, N = 4096, 4-bit M = 2 / 3 / 4
 //    12.6 / 17.3 / 17.4 against 15.7 / 25.2 / 25.3, bf16 x M = 4 18.2 against
-//    25.6, 8-bit M = 4 23.7 against 27.5; K = 16384 g128 M = 4 18.7 against
+//    25.6, 8-bit M = 4 22.3 against 27.5; K = 16384 g128 M = 4 18.7 against
 //    24.5.
 //  * 4096 < K <= 8192: M = 2 (K = N = 8192, 4-bit: 12.0 against 13.4) and
 //    2-bit codes (which no MFMA kernel takes); the decode kernel keeps 4-bit

@@ -10,6 +10,10 @@ into a later, lane-conditional block (it did once, for a per-lane select of
 the partial sums), and then the wait silently stops covering the DMA.  This
 test counts, per kernel, the register-returning buffer loads issued before
 the first `s_barrier` and checks them against the wait's count.
+
+The other checks here read the same code objects: issue order of the
+whole-line kernels, the split-K GEMM's in-flight loads, and that no kernel
+of the plugin spills registers to scratch memory.
 """
 import os
 import re
@@ -31,7 +35,8 @@ def _tool(name):
 
 
 @pytest.fixture(scope="module")
-def disassembly(tmp_path_factory):
+def code_objects(tmp_path_factory):
+    """The plugin's embedded gfx950 code objects, unpacked into a temp dir."""
     import mlx_amd
     objdump = _tool("llvm-objdump")
     if not objdump:
@@ -42,8 +47,16 @@ def disassembly(tmp_path_factory):
     shutil.copy(mlx_amd.PLUGIN_PATH, so)
     # --offloading writes the embedded device code objects next to its input
     subprocess.run([objdump, "--offloading", str(so)], cwd=d, check=True, capture_output=True)
+    cos = sorted(d.glob("plugin.so.*gfx950*"))
+    assert cos, "no gfx950 code object in the plugin"
+    return cos
+
+
+@pytest.fixture(scope="module")
+def disassembly(code_objects):
+    objdump = _tool("llvm-objdump")
     out = {}
-    for co in sorted(d.glob("plugin.so.*gfx950*")):
+    for co in code_objects:
         syms = subprocess.run([objdump, "-t", str(co)], check=True, capture_output=True, text=True).stdout
         names = [ln.split()[-1] for ln in syms.splitlines()
                  if " .text" in ln and any(k in ln for k in KERNELS + (LINE, MX, SK)) and not ln.endswith(".kd")]
@@ -144,3 +157,31 @@ def test_split_k_gemm_keeps_loads_in_flight(disassembly):
             bad.append(f"{name}: main-loop waits down to vmcnt({min(low)})")
     assert seen, "qgemm_sk_kernel not found in the plugin"
     assert not bad, "\n".join(bad[:10])
+
+
+def test_no_kernel_spills_to_scratch(code_objects):
+    """Every kernel of the plugin runs without a private (scratch) segment:
+    a register spill there turns into per-lane memory traffic and a full
+    vector-memory drain (a spilled load's value has to arrive before it can
+    be stored), and on these streaming kernels that costs more than the
+    spill saves.  Spills into the accumulator registers (no memory) are
+    allowed."""
+    readelf = _tool("llvm-readelf")
+    if not readelf:
+        pytest.skip("llvm-readelf not available")
+    seen, bad = 0, []
+    for co in code_objects:
+        notes = subprocess.run([readelf, "--notes", str(co)], check=True, capture_output=True, text=True).stdout
+        # one YAML map per kernel in .amdhsa.kernels; each holds .name and
+        # .private_segment_fixed_size
+        # (kernel entries at indent 2, their keys at 4, argument entries deeper)
+        for block in re.split(r"\n  - \.", notes):
+            name = re.search(r"^    \.name:\s+(\S+)", block, re.M)
+            priv = re.search(r"^    \.private_segment_fixed_size:\s+(\d+)", block, re.M)
+            if not name or not priv:
+                continue
+            seen += 1
+            if int(priv.group(1)):
+                bad.append(f"{name.group(1)}: {priv.group(1)} bytes of scratch per lane")
+    assert seen > 100, f"only {seen} kernels found in the code objects' metadata"
+    assert not bad, f"{len(bad)} kernels spill:\n" + "\n".join(bad[:10])

@@ -124,10 +124,12 @@ def test_split_k_gemv_parity(ctx, oracle, bits, xd, sbd, od):
     O = oracle
     # (1, 28672, 11, 32): f32 x and scales need the 4-row block form there
     # (8 rows of g32 f32 scales do not fit next to 112 KB of x); (2, 12288,
-    # 13, 32) and (2, 14336, 21, 64) run the two-row form on both x rows
+    # 13, 32) and (2, 14336, 21, 64) run the two-row form on both x rows;
+    # (1, 5120, 23, 32) and (1, 14336, 19, 32): idle lanes (masked scales)
+    # with two groups per unit
     for (M, K, N, gs) in [(1, 5120, 37, 128), (1, 8192, 50, 32), (1, 14336, 21, 64), (1, 28672, 13, 64),
                           (1, 28672, 11, 32), (1, 32768, 9, 32), (2, 14336, 21, 64), (2, 9216, 13, 128),
-                          (2, 12288, 13, 32), (2, 16384, 6, 32)]:
+                          (2, 12288, 13, 32), (2, 16384, 6, 32), (1, 5120, 23, 32), (1, 14336, 19, 32)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 17 + K + M)
         y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemv"])
         if od == F32 and K > 8192:
