@@ -49,8 +49,8 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     //    8-bit K = 12288: 17.7 against 25.3); at K <= 8192 the decode kernel
     //    is faster (K = 8192, N = 8192: 12.8 against 18.1).
     // 2..4 rows of x with K <= 16384: the K-split whole-line kernel where it
-    // applies and measured faster (qgemv_mx.h, mx_wins: every K > 8192; M = 2
-    // and 2-bit codes up to K = 8192; at K <= 4096 8-bit codes, 2-bit at
+    // applies and measured faster (qgemv_mx.h, mx_wins: f32 x; every K > 8192;
+    // M = 2 and 2-bit codes up to K = 8192; at K <= 4096 8-bit codes, 2-bit at
     // M >= 3, 4-bit at M = 2 with f16 x)
     if (args.M >= 2 && args.M <= 4) {
         const LuxStatus s = launch_mx_bits(args, st);
@@ -77,6 +77,27 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const LuxStatus s = launch_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
+    // rows m0 .. m0 + mc - 1 of x and y
+    auto rows = [&](int m0, int mc) {
+        QmmArgs a = args;
+        a.M = mc;
+        const size_t xel = args.x_dtype == DT_F32 ? 4 : 2, yel = args.out_dtype == DT_F32 ? 4 : 2;
+        a.x = static_cast<const uint8_t*>(args.x) + (size_t)m0 * args.K * xel;
+        a.y = static_cast<uint8_t*>(args.y) + (size_t)m0 * args.N * yel;
+        return a;
+    };
+    // f32 x with more than 4 rows: chunks of 4 (a last single row on the
+    // M = 1 kernels) on the K-split whole-line kernel where it applies
+    // (M = 8, K = 4096, N = 14336, 4-bit: the row-run kernel took 126.9 us)
+    if (args.x_dtype == DT_F32 && args.M > 4) {
+        for (int m0 = 0; m0 < args.M; m0 += 4) {
+            const QmmArgs a = rows(m0, args.M - m0 < 4 ? args.M - m0 : 4);
+            const LuxStatus s = a.M >= 2 ? launch_mx_bits(a, st) : launch_bits(a, st);
+            if (m0 == 0 && s == LuxStatus::NotSupported) break;  // nothing launched: the row-run kernel below
+            if (s != LuxStatus::Ok) return s;
+            if (m0 + 4 >= args.M) return LuxStatus::Ok;
+        }
+    }
     // (f32 x: at most 4 rows, the row-run kernel's registers at 8 do not fit)
     int chunk = args.x_dtype == DT_F32 ? 4 : 8;
     while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
@@ -84,12 +105,7 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     // which stages x in up to 160 KB; the row-run kernel declines it itself
     if (args.M > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) return LuxStatus::NotSupported;
     for (int m0 = 0; m0 < args.M; m0 += chunk) {
-        QmmArgs a = args;
-        a.M = args.M - m0 < chunk ? args.M - m0 : chunk;
-        const size_t xel = args.x_dtype == DT_F32 ? 4 : 2, yel = args.out_dtype == DT_F32 ? 4 : 2;
-        a.x = static_cast<const uint8_t*>(args.x) + (size_t)m0 * args.K * xel;
-        a.y = static_cast<uint8_t*>(args.y) + (size_t)m0 * args.N * yel;
-        const LuxStatus s = launch_bits(a, st);
+        const LuxStatus s = launch_bits(rows(m0, args.M - m0 < chunk ? args.M - m0 : chunk), st);
         if (s != LuxStatus::Ok) return s;
     }
     return LuxStatus::Ok;

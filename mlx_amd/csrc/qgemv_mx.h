@@ -9,8 +9,8 @@
 // RB rows, and lane l the 16 codes 16 l .. 16 l + 15 of that part.  So one
 // wave load per row reads 64 lanes x 16 codes, contiguous (512 B at 4-bit
 // codes: whole 128-byte lines), and a lane holds the x operands of its 16
-// codes for each of the MX rows of x (8 words per row at 16-bit x, where a
-// wave covering all of K = 4096 would need 32).
+// codes for each of the MX rows of x (8 words per row at 16-bit x, 16 at f32
+// x, where a wave covering all of K = 4096 would need 32 or 64).
 // Every load is issued at the start, straight into registers:
 //   1. x: the lane's 16 x values of each of the MX rows;
 //   2. the block's RB scale rows and RB bias rows (contiguous in the scale
@@ -64,7 +64,8 @@ __global__ __launch_bounds__(64 * KW) void qgemv_mx_kernel(
     constexpr int kThreads = 64 * KW;
     constexpr int OP = op_kind<BITS, TX>();
     constexpr int NC = C::NC, WPL = C::WPL;
-    constexpr int XW = NC / 2;  // 32-bit words of x per row of x (16-bit x)
+    constexpr int XE = TX == DT_F32 ? 4 : 2;
+    constexpr int XW = NC * XE / 4;  // 32-bit words of x per row of x
     constexpr int kSb = SB == DT_F32 ? 4 : 2;
     constexpr int VPB = 8 / MX;  // rows per reduction batch
     static_assert(MX == 2 || MX == 4, "rows of x");
@@ -83,11 +84,11 @@ __global__ __launch_bounds__(64 * KW) void qgemv_mx_kernel(
     // row M-1; they are never stored) ----
     uint32_t xn[MX][XW];
     {
-        const auto xr = buf_rsrc(x, (uint32_t)M * K * 2);
+        const auto xr = buf_rsrc(x, (uint32_t)M * K * XE);
 #pragma unroll
         for (int m = 0; m < MX; m++) {
             const int mr = m < M ? m : M - 1;
-            const uint32_t off = ok ? ((uint32_t)mr * K + kc) * 2u : kZeroOff;
+            const uint32_t off = ok ? ((uint32_t)mr * K + kc) * XE : kZeroOff;
 #pragma unroll
             for (int j = 0; j < XW / 4; j++) {
                 const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * j, 0, 0);
@@ -264,10 +265,12 @@ LuxStatus launch_mx_q(const QmmArgs& a, hipStream_t st) {
 // waves per block: each covers at most 1024 codes of K; 8 waves (2 per
 // SIMD, 256 VGPRs) take 16-row blocks, 16 waves (4 per SIMD, 128 VGPRs) 16
 // rows of codes up to 4 bits and 8 rows of 8-bit codes (16 rows of 8-bit
-// codes are 64 VGPRs of code words alone and spilled to scratch)
+// codes are 64 VGPRs of code words alone and spilled to scratch), half that
+// with f32 x (16 VGPRs of x per row of x)
 template <int BITS, int TX, int SB, int MX>
 LuxStatus launch_mx_r(const QmmArgs& a, hipStream_t st) {
-    if (a.K > 8192) return launch_mx_q<BITS, TX, SB, MX, BITS == 8 ? 8 : 16, 16>(a, st);
+    constexpr int RB16 = (BITS == 8 ? 8 : 16) / (TX == DT_F32 ? 2 : 1);
+    if (a.K > 8192) return launch_mx_q<BITS, TX, SB, MX, RB16, 16>(a, st);
     if (a.K > 4096) return launch_mx_q<BITS, TX, SB, MX, 16, 8>(a, st);
     return mx_rows(a.N) == 28 ? launch_mx_q<BITS, TX, SB, MX, 28, 4>(a, st) : launch_mx_q<BITS, TX, SB, MX, 16, 4>(a, st);
 }
@@ -298,13 +301,16 @@ LuxStatus launch_mx_m(const QmmArgs& a, hipStream_t st) {
 //    M >= 3 (K = 8192: 14.2 against 15.8; K = 6144 M = 3: 11.1 against 14.7)
 //    and the LDS-ring kernel 8-bit M >= 3 (K = 8192 g128 bf16 M = 4: 20.3
 //    against 24.2).
+//  * f32 x: everywhere it applies.  The only other kernel for f32 x at
+//    M >= 2 is the row-run fallback, 5-6x slower (M = 4, K = N = 4096, 4-bit:
+//    33.0 us).
 inline bool mx_wins(int bits, int M, int x_dtype, int K) {
-    if (K > 8192) return true;
+    if (x_dtype == DT_F32 || K > 8192) return true;
     if (K > 4096) return M == 2 || bits == 2;
     return bits == 8 || (bits == 2 && M >= 3) || (bits == 4 && M == 2 && x_dtype == DT_F16);
 }
 
-// 2 <= M <= 4, 16-bit x, 2/4/8-bit codes where it wins (mx_wins), K <= 16384
+// 2 <= M <= 4, 2/4/8-bit codes where it wins (mx_wins), K <= 16384
 // with each wave's part of K a whole number of 16-code chunks; NotSupported
 // otherwise
 template <int BITS>
@@ -314,11 +320,18 @@ LuxStatus launch_mx_b(const QmmArgs& a, hipStream_t st) {
     } else {
         // each wave's part of K a whole number of 16-code chunks
         const int kw = a.K > 8192 ? 16 : a.K > 4096 ? 8 : 4;
-        if (a.M < 2 || a.M > 4 || a.x_dtype == DT_F32 || a.K > 16384 || a.K % (16 * kw) != 0 ||
+        if (a.M < 2 || a.M > 4 || a.K > 16384 || a.K % (16 * kw) != 0 ||
             !mx_wins(BITS, a.M, a.x_dtype, a.K))
             return LuxStatus::NotSupported;
         // offsets within the 32-bit buffer ranges
         if ((size_t)a.N * a.K * BITS / 8 >= (1ull << 31)) return LuxStatus::NotSupported;
+        if (a.x_dtype == DT_F32) {
+            switch (a.sb_dtype) {
+            case DT_F32: return launch_mx_m<BITS, DT_F32, DT_F32>(a, st);
+            case DT_F16: return launch_mx_m<BITS, DT_F32, DT_F16>(a, st);
+            default: return launch_mx_m<BITS, DT_F32, DT_BF16>(a, st);
+            }
+        }
         if (a.x_dtype == DT_F16) {
             switch (a.sb_dtype) {
             case DT_F32: return launch_mx_m<BITS, DT_F16, DT_F32>(a, st);

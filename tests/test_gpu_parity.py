@@ -172,6 +172,30 @@ def test_kline_gemv_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"k-line b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("sbd,od", [(F32, F32), (F16, F32), (BF16, F16)])
+def test_kline_gemv_f32_x(ctx, oracle, bits, sbd, od):
+    """f32 x at 2 <= M <= 4: the K-split whole-line kernel takes every K it
+    applies to (K <= 16384, each wave's part a whole number of 16-code
+    chunks), with 4, 8 and 16 waves per block and, at 16 waves, half the
+    rows of the 16-bit x blocks (f32 x is 16 VGPRs per row of x); M = 5..9
+    in chunks of 4 rows (a last single row on the M = 1 kernels).  fp32
+    outputs with K > 8192 are gated against the oracle's fp64 accumulation
+    (the sequential fp32 oracle's own rounding reaches ~1e-5 there)."""
+    O = oracle
+    for i, (K, N, gs) in enumerate([(4096, 300, 64), (1024, 77, 32), (256, 40, 64), (2048, 7150, 128),
+                                    (6144, 100, 64), (8192, 33, 32), (14336, 70, 32), (16384, 19, 128),
+                                    (4096, 130, 64), (14336, 33, 128), (2048, 65, 32)]):
+        M = 2 + (i + bits) % 3 if i < 8 else (5, 8, 9)[i - 8]
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, F32, sbd, seed=bits * 47 + M + K)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, F32, sbd, od, KERNELS["gemv"])
+        if od == F32 and K > 8192:
+            want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F32, sbd, od, variant="f64").astype(np.float32)
+        else:
+            want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F32, sbd, od)
+        check_output(O, y, want, od, f"k-line f32 x b{bits} M{M} K{K} N{N} g{gs}")
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_small_m_mfma_parity(ctx, oracle, bits, xd, sbd, od):
