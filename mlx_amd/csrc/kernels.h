@@ -56,6 +56,9 @@ LuxStatus launch_qmm_skinny(const QmmArgs& a, hipStream_t st);
 // MFMA decode kernel for 2 <= M <= 8, 4-bit codes, f16/bf16 x, K % 1024 == 0,
 // K <= 8192; NotSupported otherwise (tried first)
 LuxStatus launch_qgemv_dec(const QmmArgs& a, hipStream_t st);
+// 4x4x4-MFMA decode kernel (256-byte row segments) for 2 <= M <= 8, 4-bit
+// codes, f16/bf16 x, K = 2048, 4096 or 8192; NotSupported otherwise
+LuxStatus launch_qgemv_q4(const QmmArgs& a, hipStream_t st);
 // MFMA kernel with LDS operand rings for 2 <= M <= 16, 4/8-bit codes,
 // f16/bf16 x, K % 1024 == 0; NotSupported otherwise (tried before the above)
 LuxStatus launch_qgemv_mid(const QmmArgs& a, hipStream_t st);

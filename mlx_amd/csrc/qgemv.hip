@@ -52,6 +52,17 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     // applies and measured faster (qgemv_mx.h, mx_wins: f32 x; every K > 8192;
     // M = 2 and 2-bit codes up to K = 8192; at K <= 4096 8-bit codes, 2-bit at
     // M >= 3, 4-bit at M = 2 with f16 x)
+    // 4-bit codes: the 4x4x4-MFMA decode kernel (K = 2048, 4096, 8192) at
+    // M <= 4, and at M = 5..8 with K = 4096 (two x sets; at K = 2048 and
+    // 8192 the decode kernel stays faster there).  Same box, us per launch
+    // against the kernels AUTO picked before: K = 4096, N = 14336, M = 2 / 3
+    // / 4 / 6 / 8 8.8 / 9.1 / 9.0 / 11.7 / 12.1 against 10.2 / 12.1 / 12.2 /
+    // 12.6 / 13.0; K = N = 8192 M = 4 12.2 against 13.8 (M = 8 20.1 against
+    // 15.0); K = 2048, N = 8192, M = 8 5.6 against 5.4
+    if (args.M >= 2 && args.bits == 4 && (args.M <= 4 || (args.M <= 8 && args.K == 4096))) {
+        const LuxStatus s = launch_qgemv_q4(args, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
     if (args.M >= 2 && args.M <= 4) {
         const LuxStatus s = launch_mx_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;

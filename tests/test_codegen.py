@@ -26,6 +26,7 @@ LLVM = "/opt/rocm/llvm/bin"
 KERNELS = ("qgemv_stream_kernel", "qgemv_split_kernel", "qgemv_dec_kernel", "qmm_skinny_kernel")
 LINE = "qgemv_line_kernel"
 MX = "qgemv_mx_kernel"
+Q4 = "qgemv_q4_kernel"
 SK = "qgemm_sk_kernel"
 
 
@@ -59,7 +60,7 @@ def disassembly(code_objects):
     for co in code_objects:
         syms = subprocess.run([objdump, "-t", str(co)], check=True, capture_output=True, text=True).stdout
         names = [ln.split()[-1] for ln in syms.splitlines()
-                 if " .text" in ln and any(k in ln for k in KERNELS + (LINE, MX, SK)) and not ln.endswith(".kd")]
+                 if " .text" in ln and any(k in ln for k in KERNELS + (LINE, MX, Q4, SK)) and not ln.endswith(".kd")]
         if not names:
             continue
         dis = subprocess.run([objdump, "-d", "--mcpu=gfx950", "--disassemble-symbols=" + ",".join(names), str(co)],
@@ -79,7 +80,7 @@ def test_weight_loads_precede_their_wait(disassembly):
     found = {k: 0 for k in KERNELS}
     bad = []
     for name, lines in disassembly.items():
-        if LINE in name or MX in name or SK in name:
+        if LINE in name or MX in name or Q4 in name or SK in name:
             continue
         loads, vm = 0, None
         for t in lines:
@@ -101,18 +102,20 @@ def test_weight_loads_precede_their_wait(disassembly):
 
 
 def test_line_kernel_issue_order(disassembly):
-    """The whole-line kernels (M = 1, and the K-split one for 2..4 rows of x):
+    """The whole-line kernels (M = 1, and the K-split one for 2..4 rows of x)
+    and the 4x4x4-MFMA decode kernel, which loads in the same order:
     x and scale loads (default cache policy) all issue before the block
     barrier, the non-temporal code loads all after it and before the first
     wait on a vector-memory load -- so the x and scale requests of every wave
     precede the codes in the CU's queue, and no code load was moved behind
     the arithmetic."""
-    seen, seen_mx, bad = 0, 0, []
+    seen, seen_mx, seen_q4, bad = 0, 0, 0, []
     for name, lines in disassembly.items():
-        if LINE not in name and MX not in name:
+        if LINE not in name and MX not in name and Q4 not in name:
             continue
         seen += 1
         seen_mx += MX in name
+        seen_q4 += Q4 in name
         bar = next((i for i, t in enumerate(lines) if t.startswith("s_barrier")), None)
         if bar is None:
             bad.append(f"{name}: no barrier")
@@ -128,7 +131,7 @@ def test_line_kernel_issue_order(disassembly):
             bad.append(f"{name}: {len(late)} loads after the first vmcnt wait")
         if not any(t.startswith("buffer_load") and re.search(r"\bnt\b", t) for t in after[:wait]):
             bad.append(f"{name}: no code load between the barrier and the first wait")
-    assert seen and seen_mx, "qgemv_line_kernel or qgemv_mx_kernel not found in the plugin"
+    assert seen and seen_mx and seen_q4, "qgemv_line_kernel, qgemv_mx_kernel or qgemv_q4_kernel not found in the plugin"
     assert not bad, "\n".join(bad[:10])
 
 

@@ -172,6 +172,24 @@ def test_kline_gemv_parity(ctx, oracle, bits, xd, sbd, od):
         check_output(O, y, want, od, f"k-line b{bits} M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32),
+                                       (F16, BF16, F32)])
+def test_q4_decode_parity(ctx, oracle, xd, sbd, od):
+    """2 <= M <= 8 rows of x with 4-bit codes and K = 2048, 4096 or 8192 run
+    the 4x4x4-MFMA decode kernel: one and two sets of 4 x rows (M = 5..7
+    carry x rows that are never stored), 4, 8 and 16 waves, 16- and 28-row
+    blocks (N = 7150: 256 blocks of 28, the last ragged), every group size,
+    N not a multiple of the 4-row group."""
+    O = oracle
+    for (M, K, N, gs) in [(2, 4096, 300, 64), (3, 2048, 77, 32), (4, 8192, 130, 128), (5, 4096, 33, 32),
+                          (6, 2048, 7150, 64), (7, 8192, 41, 64), (8, 4096, 7150, 128), (8, 2048, 19, 32),
+                          (4, 4096, 14336, 64)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, 4, gs, xd, sbd, seed=M * 53 + K + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od, KERNELS["gemv"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od)
+        check_output(O, y, want, od, f"q4 M{M} K{K} N{N} g{gs}")
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("sbd,od", [(F32, F32), (F16, F32), (BF16, F16)])
 def test_kline_gemv_f32_x(ctx, oracle, bits, sbd, od):
