@@ -200,8 +200,9 @@ __attribute__((visibility("default"))) bool lux_gpu_backend_quant_init(const lux
  * current device holding at least the bytes the shape needs (not checked:
  * there are no buffer sizes here); `stream` is a hipStream_t of that device
  * (NULL: the null stream).  Same kernels, selection, results and shape and
- * dtype errors as op_quantized_matmul_ex.  The split-K small-M GEMM's
- * partial sums and tile counters live in a 16 MiB static device array that
+ * dtype errors as op_quantized_matmul_ex.  The partial sums, tile counters
+ * and flags of the split-K small-M GEMM and of the large GEMM's split last
+ * round live in a 16 MiB (+ 4 KiB) static device array that
  * each GPU holds until the process ends (shapes whose split would need more
  * are INVALID_ARGUMENT; the split rule keeps every shape within it).  All
  * calls on one GPU share that array: calls that overlap in time on one GPU

@@ -34,8 +34,9 @@ struct HipContext {
     char name[256] = {0};
     int compute_units = 0;
     int max_wg = 0;
-    // kernel workspace (partial sums and self-resetting tile counters of the
-    // split-K GEMM), allocated and zeroed once here so that no launch
+    // kernel workspace (partial sums and self-resetting tile counters and
+    // flags of the split-K small-M GEMM and of the large GEMM's split last
+    // round), allocated and zeroed once here so that no launch
     // allocates; used only by work on `stream`, which orders its users
     void* ws = nullptr;
     size_t ws_bytes = 0;

@@ -72,11 +72,12 @@ LuxStatus launch_qgemm_sk(const QmmArgs& a, hipStream_t st);
 // workspace bytes launch_qgemm_sk uses for this shape given `cap` bytes
 // (0: it needs none or does not apply)
 size_t qgemm_sk_workspace(int M, int K, int N, int bits, int x_dtype, size_t cap);
-// the workspace every caller of the split-K GEMM provides (a context's, or
-// the allocation-free entry point's static one): the same size everywhere,
-// so the same shape takes the same split, and the same result bits
-// (16 MiB of partials for the largest split, 512 blocks of 32 KiB, and the
-// tile counters)
+// the workspace every caller of the GEMMs provides (a context's, or the
+// allocation-free entry point's static one): the same size everywhere, so
+// the same shape takes the same split, and the same result bits.  16 MiB of
+// partials: the split-K small-M GEMM's largest split (512 blocks of 32 KiB),
+// and the large GEMM's split last round (at most 128 tiles, one K half of
+// 128 KiB each).  The first KiB holds tile counters and flags.
 constexpr size_t kSplitWorkspaceBytes = (16u << 20) + 4096;
 // MFMA GEMM for f16/bf16 activations; needs K % 64 == 0
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st);

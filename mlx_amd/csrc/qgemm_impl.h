@@ -34,7 +34,14 @@
 //
 // Grid: one block per tile, M-tile fastest.  Blocks are dealt round-robin to
 // the 8 XCDs, so with 8 M-tiles (M = 2048) every XCD owns one 256-row slab of
-// x and keeps it in its own L2 while it walks the N-tiles.
+// x and keeps it in its own L2 while it walks the N-tiles.  When the tiles
+// leave a last round at most half full (tiles % 256 in 1..128, e.g. 896
+// tiles at M = 2048, N = 14336: 3.5 rounds), each tile of that round is run
+// by two blocks over the two halves of K, so the last round fills the CUs
+// and takes half as long; the two halves' fp32 sums meet in the workspace
+// (the second block to finish adds the first's partial tile to its own --
+// one fp32 addition per value, the same whichever finishes first -- and
+// stores y).
 #pragma once
 #include "kernels.h"
 #include "qcommon.h"
@@ -55,6 +62,17 @@ constexpr int kThreads = 512;  // 8 waves: two per SIMD
 constexpr int kXStageBytes = BM * BK * 2;  // 32768
 constexpr int kXStages = 3;
 constexpr int kWStageBytes = BN * BK * 2;  // 16384
+// tail split: CUs of the target (MI355X: 256), the workspace layout (tile
+// counters in its first KiB, shared with the split-K small-M GEMM, which
+// never runs at the same time on a context; partial tiles from 4 KiB on)
+constexpr int kCUs = 256;
+constexpr uint32_t kSplitSlotBytes = BM * BN * 4;  // one K half of one tile, fp32
+constexpr size_t kSplitPartOffset = 4096;
+constexpr int kSplitFlagWord = 128;                 // flags after the 128 counters
+constexpr int kCachePolicyDevice = 16;             // buffer cache policy sc1
+static_assert(kSplitPartOffset + (size_t)kCUs / 2 * kSplitSlotBytes <= kSplitWorkspaceBytes, "workspace size");
+static_assert(kCUs / 2 <= kSplitFlagWord && (kSplitFlagWord + kCUs / 2) * 4 <= 1024,
+              "split-tile counters and flags within the first KiB");
 
 // chunk position permutation of LDS row r (bijective on the 8 chunks; rows
 // r and r + 8 get different permutations)
@@ -324,6 +342,7 @@ struct Ctx {
     const uint32_t* wq;
     uint32_t xoff[4];   // byte offset (in x) of this lane's 4 x chunks, K step 0
     int wave, lane, KT, n0, N, G;
+    int k0;             // the block's first K step (K steps k0 .. k0 + KT - 1)
     uint32_t row_bytes;
     int a_row, b_row;
     int chk[4];         // byte offset of this lane's fragment chunk, per k sub-step
@@ -432,7 +451,7 @@ __device__ __forceinline__ void main_loop(f32x16 (&acc)[2][2], const Ctx& t, con
             const int off = 64 * WD::E * j + WD::E * t.lane;  // byte in the wave's 32 rows
             const int row = off / pack_row_bytes<BITS>(), byte = off % pack_row_bytes<BITS>();
             const int n = min(t.n0 + 32 * t.wave + row, t.N - 1);  // rows past N: valid data, never stored
-            wv[j] = (uint32_t)n * t.row_bytes + (uint32_t)byte;
+            wv[j] = (uint32_t)n * t.row_bytes + (uint32_t)t.k0 * pack_row_bytes<BITS>() + (uint32_t)byte;
         }
     } else {
 #pragma unroll
@@ -441,7 +460,8 @@ __device__ __forceinline__ void main_loop(f32x16 (&acc)[2][2], const Ctx& t, con
             const int a = d / (32 * Wn::kWords), rem = d % (32 * Wn::kWords);
             const int row = rem / Wn::kWords, word = rem % Wn::kWords;
             const int n = min(t.n0 + 32 * (t.wave - 4) + row, t.N - 1);
-            sp[j] = static_cast<const uint8_t*>(a ? biases : scales) + (size_t)n * t.G * Wn::kSb + 4 * word;
+            sp[j] = static_cast<const uint8_t*>(a ? biases : scales) + (size_t)n * t.G * Wn::kSb +
+                    (size_t)(t.k0 / 4) * Wn::kRowBytes + 4 * word;
         }
     }
 
@@ -494,13 +514,22 @@ template <int TX, int BITS, int SB, int GS, bool EPI>
 __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep,
-    int mtiles) {
+    int mtiles, int split_from, void* __restrict__ ws) {
     static_assert(lds_fits<BITS, GS, SB>(), "LDS budget");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves, 64 x 64 each
-    const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
+    // blocks below split_from own a whole tile; the rest are the two K
+    // halves (part 0: all first halves, then part 1) of tiles split_from ..
+    int tile = blockIdx.x, part = -1, KT = K / BK;
+    if (tile >= split_from) {
+        const int r = (int)((gridDim.x - (unsigned)split_from) >> 1), i = tile - split_from;
+        part = i >= r;
+        tile = split_from + i - part * r;
+        KT >>= 1;
+    }
+    const int mt = tile % mtiles, nt = tile / mtiles;
     const int m0 = mt * BM;
 
     Ctx t;
@@ -510,7 +539,8 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     t.wq = wq;
     t.wave = wave;
     t.lane = lane;
-    t.KT = K / BK;
+    t.KT = KT;
+    t.k0 = part > 0 ? KT : 0;
     t.n0 = nt * BN;
     t.N = N;
     t.G = K / GS;
@@ -521,7 +551,7 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     for (int i = 0; i < 4; i++) {
         const int r = 8 * (4 * wave + i) + (lane >> 3);
         const int rg = min(m0 + r, M - 1);  // rows past M: valid data, never stored
-        t.xoff[i] = ((uint32_t)rg * K + (((lane & 7) ^ swz(r)) << 3)) * 2;
+        t.xoff[i] = ((uint32_t)rg * K + (uint32_t)t.k0 * BK + (((lane & 7) ^ swz(r)) << 3)) * 2;
     }
     // fragment addressing: lane reads row (lane % 32), k block 8 (lane / 32)
     const int fr_row = lane & 31, kh = lane >> 5;
@@ -544,6 +574,77 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
         main_loop<TX, BITS, SB, GS, 0>(acc, t, scales, biases);
     else
         main_loop<TX, BITS, SB, GS, 1>(acc, t, scales, biases);
+
+    if (part >= 0) {
+        // A K half of a split tile.  The two halves count in on the tile's
+        // counter; the first stores its fp32 sums into slot (split tile) of
+        // the workspace -- vector q of thread tid at byte ((slot * 16 + q) *
+        // 512 + tid) * 16 -- and then raises the tile's flag; the second
+        // waits for the flag, adds those sums to its own and stores y.  The
+        // wait is for a block that has already counted in, so it is resident
+        // and past its K loop, with nothing left to wait for itself.  The
+        // sums, counters and flags are written and read with the
+        // device-scope cache policy (sc1): the halves may run on different
+        // XCDs, whose L2s are not coherent with each other.
+        const int st = tile - split_from;
+        uint32_t* counters = static_cast<uint32_t*>(ws);
+        uint32_t* flags = counters + kSplitFlagWord;
+        const __amdgpu_buffer_rsrc_t pr = make_rsrc(static_cast<uint8_t*>(ws) + kSplitPartOffset,
+                                                    (uint32_t)((gridDim.x - (unsigned)split_from) >> 1) * kSplitSlotBytes);
+        const uint32_t voff = (uint32_t)tid * 16u;
+        // the count's outcome goes through the first LDS word: every wave's
+        // transfers have landed (the K loop ends waiting for them all), so
+        // nothing writes the x stages any more (a static LDS variable would
+        // push the buffers that fill the 160 KB exactly past the limit)
+        uint32_t* word = reinterpret_cast<uint32_t*>(lds);
+        __syncthreads();
+        if (tid == 0)
+            *word = __hip_atomic_fetch_add(&counters[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*word == 0u) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const f32x16& a = acc[q >> 3][(q >> 2) & 1];
+                const int v = 4 * (q & 3);
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v4{__float_as_uint(a[v]), __float_as_uint(a[v + 1]), __float_as_uint(a[v + 2]),
+                       __float_as_uint(a[v + 3])},
+                    pr, voff, (uint32_t)(st * 16 + q) * (kThreads * 16u), kCachePolicyDevice);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(&flags[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        // the second half: wait for the first's sums (bounded: a flag never
+        // raised within ~2^22 polls marks the tile NaN instead of hanging),
+        // then set the counter and the flag back to zero for the next launch
+        if (tid == 0) {
+            uint32_t polls = 0;
+            while (__hip_atomic_load(&flags[st], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
+                   ++polls < (1u << 22))
+                __builtin_amdgcn_s_sleep(2);
+            *word = polls < (1u << 22) ? 1u : 2u;
+            __hip_atomic_store(&flags[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&counters[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        const float fail = *word == 1u ? 0.f : __builtin_nanf("");
+        v4 o[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++)
+            o[q] = __builtin_amdgcn_raw_buffer_load_b128(pr, voff, (uint32_t)(st * 16 + q) * (kThreads * 16u),
+                                                         kCachePolicyDevice);
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            f32x16& a = acc[q >> 3][(q >> 2) & 1];
+            const int v = 4 * (q & 3);
+            a[v] += __uint_as_float(o[q].x) + fail;
+            a[v + 1] += __uint_as_float(o[q].y) + fail;
+            a[v + 2] += __uint_as_float(o[q].z) + fail;
+            a[v + 3] += __uint_as_float(o[q].w) + fail;
+        }
+    }
 
     // ---- epilogue: 32x32 accumulator layout: lane holds column (lane % 32),
     // VGPR v holds row 8 (v / 4) + 4 (lane / 32) + v % 4 ----
@@ -593,9 +694,18 @@ LuxStatus launch4_e(const QmmArgs& a, hipStream_t st) {
             reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (attr != hipSuccess) return LuxStatus::Internal;
         const int mtiles = (a.M + BM - 1) / BM, ntiles = (a.N + BN - 1) / BN;
-        hipLaunchKernelGGL(kern, dim3(mtiles * ntiles), dim3(kThreads), lds, st,
+        const int tiles = mtiles * ntiles;
+        // the last round's tiles in two K halves where that round is at most
+        // half full (each half a whole number of 4-step scale windows)
+        const int r = tiles % kCUs;
+        const int split_from =
+            r > 0 && 2 * r <= kCUs && (a.K / BK) % 8 == 0 && a.ws != nullptr &&
+                    a.ws_bytes >= kSplitPartOffset + (size_t)r * kSplitSlotBytes
+                ? tiles - r
+                : tiles;
+        hipLaunchKernelGGL(kern, dim3(tiles + (tiles - split_from)), dim3(kThreads), lds, st,
                            static_cast<const uint16_t*>(a.x), a.wq, a.scales, a.biases, a.y, a.M, a.K,
-                           a.N, a.epi(), mtiles);
+                           a.N, a.epi(), mtiles, split_from, a.ws);
         return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
     }
 }

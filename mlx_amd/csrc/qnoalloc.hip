@@ -3,12 +3,13 @@
 // lux_gpu_quantized_matmul_noalloc runs op_quantized_matmul_ex's kernels on
 // caller-owned device pointers and a caller stream, with no context: it
 // calls no allocating routine, for callers that cannot (code under graph
-// capture, serving loops that forbid allocation).  The one kernel that
-// needs device memory beyond its operands, the split-K small-M GEMM (its
-// partial sums and tile counters), takes it from `scratch` below: a static
-// device array that each GPU holds from module load until the process ends.
-// Its size is the context workspace's, so a shape takes the same K split,
-// and gives the same bits, on both entry points.
+// capture, serving loops that forbid allocation).  The kernels that need
+// device memory beyond their operands -- the split-K small-M GEMM and the
+// large GEMM's split last round (partial sums, tile counters and flags) --
+// take it from `scratch` below: a static device array that each GPU holds
+// from module load until the process ends.  Its size is the context
+// workspace's, so a shape takes the same K split, and gives the same bits,
+// on both entry points.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -32,7 +33,7 @@ __global__ void clear_words(uint32_t* p, size_t n) {
 
 // once per device, with that device current: look up the array's device
 // address and clear it (a kernel on `st`, ordered before this call's work;
-// the split-K GEMM returns its counters to zero after every launch)
+// the GEMMs return their counters and flags to zero after every launch)
 LuxBackendError scratch_on(int dev, hipStream_t st, void** out) {
     std::lock_guard<std::mutex> lock(g_mu);
     if (g_scratch[dev] == nullptr) {

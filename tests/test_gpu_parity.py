@@ -579,6 +579,34 @@ def test_config3_prefill(ctx, oracle, N):
         assert dev < (2.5e-3 if od == F32 else 2.5e-3 + 2.0 ** -8)
 
 
+def test_gemm_split_last_round(ctx, oracle):
+    """The large GEMM runs a last round that is at most half full as two K
+    halves per tile, meeting in the context's workspace: 16 tiles (all
+    split), then 264 tiles (the last 8 split: one column of tiles, all M
+    tiles), then the first shape again.  Each tile counter must be back at
+    zero after its launch, and a split result equals the oracle's
+    dequantize-to-bf16 form as the unsplit tiles do; the first shape's
+    repeat is bit-identical to its first run."""
+    O = oracle
+    A = (512, 1024, 1024)
+    B = (2048, 512, 4224)
+    first = None
+    for i, (M, K, N) in enumerate([A, B, A]):
+        print(f"[case] split last round launch {i} M={M} K={K} N={N}", flush=True)
+        x, w_q, s, b, _ = O.make_problem(M, K, N, 4, 64, BF16, BF16, seed=950 + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, 64, 4, BF16, BF16, F32, KERNELS["gemm"])
+        rows = np.arange(M) if M <= 512 else np.sort(np.random.default_rng(N).choice(M, 64, replace=False))
+        xs = np.ascontiguousarray(x[rows])
+        want = O.quantized_matmul(xs, w_q, s, b, len(rows), K, N, 64, 4, BF16, BF16, F32, variant="omp",
+                                  w_round=BF16)
+        check_output(O, np.ascontiguousarray(y[rows]), want, F32, f"split last round launch {i} N={N}")
+        if (M, K, N) == A:
+            if first is None:
+                first = y
+            else:
+                assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), "repeat differs"
+
+
 # ---- fused output stage (bias + activation in the kernel's store) ---------
 
 FUSED_CASES = [
