@@ -244,7 +244,7 @@ __device__ __host__ __forceinline__ int x_swz(int u) {
     return XE == 4 ? (u & 15) : ((u & 7) ^ ((u >> 3) & 1));
 }
 
-enum : int { OP_SUB4 = 0, OP_SUB8 = 1, OP_MAGIC = 2, OP_BF16U8 = 3, OP_F32 = 4 };
+enum : int { OP_SUB4 = 0, OP_SUB8 = 1, OP_MAGIC = 2, OP_BF16U8 = 3, OP_F32 = 4, OP_SUB3 = 5, OP_SUB6 = 6 };
 template <int BITS, int TX>
 constexpr int op_kind() {
     return TX == DT_F32 ? OP_F32
@@ -380,7 +380,7 @@ __device__ __forceinline__ void prep_x(const uint8_t* lx, int sw, XOps<BITS, TX,
 
 // factor that turns the reduced lane partials into y
 template <int OP>
-constexpr float out_scale() { return (OP == OP_SUB4 || OP == OP_SUB8) ? 0x1p24f : 1.f; }
+constexpr float out_scale() { return (OP == OP_SUB4 || OP == OP_SUB8 || OP == OP_SUB3 || OP == OP_SUB6) ? 0x1p24f : 1.f; }
 
 // partial of one row for one row of x.  TWO (group size 32): s0/b0 cover
 // codes 0..31 and s1/b1 codes 32..63; otherwise one group covers the unit

@@ -53,6 +53,15 @@ struct LineCfg {
 };
 
 typedef uint32_t v3u32 __attribute__((ext_vector_type(3)));
+
+// Operand form of the whole-line kernel: op_kind's, except 3- and 6-bit
+// codes with f16 x, which take the subnormal form too (OP_SUB3 / OP_SUB6,
+// line_partial): about 1.4 / 2 VALU per code against 2.7 for the
+// magic-number pairs.
+template <int BITS, int TX>
+constexpr int line_op() {
+    return (BITS == 3 && TX == DT_F16) ? OP_SUB3 : (BITS == 6 && TX == DT_F16) ? OP_SUB6 : op_kind<BITS, TX>();
+}
 constexpr int kCachePolicyNT = 2;  // buffer-load cache policy bit: non-temporal
 
 // x operands of one chunk of NC_ codes (default: the whole-line chunk)
@@ -87,9 +96,10 @@ __device__ __forceinline__ void prep_line_x(const uint32_t* nat, LineX<BITS, TX,
             if (i < NW / 2) a = dot2(nat[i], one2, a, TX);
             else b = dot2(nat[i], one2, b, TX);
         }
-        if constexpr (OP == OP_SUB4) {
-            // code word j covers x[8j..8j+7] = nat[4j..4j+3]; operand pairs
-            // (x0,x4) (x1,x5) (x2,x6) (x3,x7) [mask 0xF, mask 0xF0, >>8 then the same]
+        if constexpr (OP == OP_SUB4 || OP == OP_SUB3) {
+            // code word (4-bit) or 24-bit group (3-bit) j covers x[8j..8j+7] =
+            // nat[4j..4j+3]; operand pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+            // [4-bit: mask 0xF, mask 0xF0, >>8 then the same]
 #pragma unroll
             for (int j = 0; j < NC / 8; j++) {
                 o.v[4 * j]     = __builtin_amdgcn_perm(nat[4 * j + 2], nat[4 * j], 0x05040100u);
@@ -99,8 +109,9 @@ __device__ __forceinline__ void prep_line_x(const uint32_t* nat, LineX<BITS, TX,
             }
             a *= 0x1p-24f;
             b *= 0x1p-24f;
-        } else if constexpr (OP == OP_SUB8) {
-            // code word j covers x[4j..4j+3] = nat[2j], nat[2j+1]: (x0,x2) (x1,x3)
+        } else if constexpr (OP == OP_SUB8 || OP == OP_SUB6) {
+            // code word (8-bit) or 24-bit group (6-bit) j covers x[4j..4j+3] =
+            // nat[2j], nat[2j+1]: (x0,x2) (x1,x3)
 #pragma unroll
             for (int j = 0; j < NC / 4; j++) {
                 o.v[2 * j]     = __builtin_amdgcn_perm(nat[2 * j + 1], nat[2 * j], 0x05040100u);
@@ -150,6 +161,43 @@ __device__ __forceinline__ float line_partial(const uint32_t* w, const LineX<BIT
             c = dot2(xo.v[4 * j + 3], w8 & 0x00F000F0u, c, DT_F16);
         }
         return fmaf(s0, fmaf(c, 0.0625f, a), b0 * (xo.h0 + xo.h1));
+    } else if constexpr (OP == OP_SUB3) {
+        // The chunk's 96 bits as four 24-bit groups of 8 codes.  Per group,
+        // t keeps codes 0..3 in its low half at bits 0, 3, 6, 9 and moves
+        // codes 4..7 to the same places of its high half; a mask then leaves
+        // one pair (code j, code 4 + j) as two f16 subnormals q 2^(p-24) at
+        // bit p = 0, 3, 6 (pair 3, at bit 9, is shifted down to 0 first: a
+        // code above bit 7 would reach the exponent field).  One accumulator
+        // per position, combined as a0 + a3 / 8 + a6 / 64.
+        static_assert(WPI == 3 && NC == 32, "3-bit chunks");
+        const uint32_t g[4] = {w[0], __builtin_amdgcn_alignbit(w[1], w[0], 24),
+                               __builtin_amdgcn_alignbit(w[2], w[1], 16), w[2] >> 8};
+        float a0 = 0.f, a3 = 0.f, a6 = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t t = (g[q] & 0x0000FFFFu) | ((g[q] << 4) & 0xFFFF0000u);
+            a0 = dot2(xo.v[4 * q], t & 0x00070007u, a0, DT_F16);
+            a3 = dot2(xo.v[4 * q + 1], t & 0x00380038u, a3, DT_F16);
+            a6 = dot2(xo.v[4 * q + 2], t & 0x01C001C0u, a6, DT_F16);
+            a0 = dot2(xo.v[4 * q + 3], (t >> 9) & 0x00070007u, a0, DT_F16);
+        }
+        return fmaf(s0, fmaf(a6, 0.015625f, fmaf(a3, 0.125f, a0)), b0 * (xo.h0 + xo.h1));
+    } else if constexpr (OP == OP_SUB6) {
+        // Four 24-bit groups of 4 codes; t as for 3-bit codes (codes 0, 1 in
+        // the low half at bits 0, 6; codes 2, 3 at the same places of the
+        // high half).  Pair (0, 2) by a mask, pair (1, 3) shifted down to
+        // bit 0 first: both f16 subnormals q 2^-24, one accumulator.
+        static_assert(WPI == 3 && NC == 16, "6-bit chunks");
+        const uint32_t g[4] = {w[0], __builtin_amdgcn_alignbit(w[1], w[0], 24),
+                               __builtin_amdgcn_alignbit(w[2], w[1], 16), w[2] >> 8};
+        float d = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t t = (g[q] & 0x0000FFFFu) | ((g[q] << 4) & 0xFFFF0000u);
+            d = dot2(xo.v[2 * q], t & 0x003F003Fu, d, DT_F16);
+            d = dot2(xo.v[2 * q + 1], (t >> 6) & 0x003F003Fu, d, DT_F16);
+        }
+        return fmaf(s0, d, b0 * (xo.h0 + xo.h1));
     } else if constexpr (OP == OP_SUB8) {
         float d = 0.f;
 #pragma unroll
@@ -226,7 +274,7 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int K, int N, int gshift, Epilogue ep) {
     using C = LineCfg<BITS>;
-    constexpr int OP = op_kind<BITS, TX>();
+    constexpr int OP = line_op<BITS, TX>();
     constexpr int XE = TX == DT_F32 ? 4 : 2;
     constexpr int kSb = SB == DT_F32 ? 4 : 2;
     constexpr int NC = C::NC, WPI = C::WPI;
