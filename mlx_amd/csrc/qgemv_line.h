@@ -209,10 +209,29 @@ __device__ __forceinline__ float line_partial(const uint32_t* w, const LineX<BIT
         return fmaf(s0, d, b0 * (xo.h0 + xo.h1));
     } else if constexpr (OP == OP_F32) {
         float d0 = 0.f, d1 = 0.f;
+        if constexpr (BITS == 4) {
+            // nibble planes: code 2e of a word is byte e of lo, code 2e + 1
+            // byte e of hi, each one v_cvt_f32_ubyte{e} (the asm keeps the
+            // compiler from folding the masks back into an extract per
+            // code); same codes, same FMA order as the generic form
 #pragma unroll
-        for (int i = 0; i < NC / 2; i++) d0 = fmaf(__uint_as_float(xo.v[i]), (float)unit_code<BITS>(w, i), d0);
+            for (int j = 0; j < WPI; j++) {
+                uint32_t lo = w[j] & 0x0F0F0F0Fu, hi = (w[j] >> 4) & 0x0F0F0F0Fu;
+                asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
-        for (int i = NC / 2; i < NC; i++) d1 = fmaf(__uint_as_float(xo.v[i]), (float)unit_code<BITS>(w, i), d1);
+                for (int e = 0; e < 4; e++) {
+                    const int i = 8 * j + 2 * e;
+                    float& d = i < NC / 2 ? d0 : d1;
+                    d = fmaf(__uint_as_float(xo.v[i]), (float)((lo >> (8 * e)) & 0xffu), d);
+                    d = fmaf(__uint_as_float(xo.v[i + 1]), (float)((hi >> (8 * e)) & 0xffu), d);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NC / 2; i++) d0 = fmaf(__uint_as_float(xo.v[i]), (float)unit_code<BITS>(w, i), d0);
+#pragma unroll
+            for (int i = NC / 2; i < NC; i++) d1 = fmaf(__uint_as_float(xo.v[i]), (float)unit_code<BITS>(w, i), d1);
+        }
         if constexpr (TWO) return (s0 * d0 + b0 * xo.h0) + (s1 * d1 + b1 * xo.h1);
         else return s0 * (d0 + d1) + b0 * (xo.h0 + xo.h1);
     } else {
