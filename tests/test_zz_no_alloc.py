@@ -3,9 +3,10 @@ through the C ABI on raw device pointers and a caller stream, against the
 context op op_quantized_matmul_ex on the same inputs: bit for bit (the same
 kernels, and the same K split, since its static scratch is the size of a
 context's workspace), and within the output gate of the oracle.  Two calls
-in a row share the scratch, the second with a smaller input; the large one
-runs the split-K GEMM with its parts meeting in the scratch, so a counter
-left nonzero by the first call would break the second.
+in a row share the scratch, the second with a smaller input; the first two
+run the split-K GEMM with its parts meeting in the scratch, the next two the
+large GEMM with the two K halves of its tiles meeting there, so a counter or
+flag left nonzero by one call would break the next.
 """
 import ctypes
 import os
@@ -21,6 +22,8 @@ pytestmark = pytest.mark.gpu
 CALLS = [
     (64, 3584, 4096, 3, 64, F16, F16, F16, 0),     # split-K GEMM, 7 K parts, 224 blocks
     (17, 1152, 200, 4, 32, BF16, BF16, F32, 2),    # split-K GEMM, 3 K parts, 6 blocks
+    (512, 1024, 1024, 4, 64, BF16, BF16, F32, 2),  # large GEMM, 16 tiles, each in two K halves
+    (300, 512, 200, 4, 64, F16, F16, F16, 2),      # large GEMM, 4 ragged tiles, each in two K halves
     (1, 4096, 512, 4, 64, F16, F16, F16, 0),       # a GEMV: no scratch
 ]
 
