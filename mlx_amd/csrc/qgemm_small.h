@@ -80,35 +80,103 @@ __device__ __forceinline__ uint32_t pack_t(float a, float b) {
     }
 }
 
-// codes 8s .. 8s+7 of the lane's 32 (held in BITS words) dequantized to T:
-// the B operand of sub-step s
+// the f16 in the low / high half of a word, as fp32 (v_fma_mix_f32 reads it
+// in place when the product feeds an FMA)
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float half_lo(uint32_t m) { return (float)__builtin_bit_cast(f16x2_t, m)[0]; }
+__device__ __forceinline__ float half_hi(uint32_t m) { return (float)__builtin_bit_cast(f16x2_t, m)[1]; }
+
+// the 24 bits at bit offset O of a lane's code words (a funnel shift where
+// they straddle two words)
+template <int O>
+__device__ __forceinline__ uint32_t bits24(const uint32_t* c) {
+    constexpr int wi = O / 32, sh = O % 32;
+    if constexpr (sh + 24 <= 32) return c[wi] >> sh;
+    else return __builtin_amdgcn_alignbit(c[wi + 1], c[wi], sh);
+}
+// a 24-bit group with its low 16 bits kept and bits 12..27 moved to the
+// high half: the codes of the group's second half land at the bit positions
+// of the first half's codes
+__device__ __forceinline__ uint32_t fold24(uint32_t g) { return (g & 0x0000FFFFu) | ((g << 4) & 0xFFFF0000u); }
+
+// codes 8s .. 8s+7 of the lane's 64 (held in 2 BITS words) dequantized to T:
+// the B operand of sub-step s.
+//
+// 3/4/6/8-bit codes: masks leave pairs of codes in place in the two halves
+// of a word, i.e. as the f16 subnormals q 2^(p-24) (p = the code's bit
+// position within its half, p + BITS <= 10), and v_fma_mix_f32 computes
+// fma(s 2^(24-p), q 2^(p-24), b) from them: the product is exactly s q, so
+// each value is fmaf(s, q, b), bit for bit, in one instruction instead of a
+// convert and an FMA.  (2^(24-p) s is exact for |s| < 2^103: any larger
+// scale, from weights of range above ~1e32, would overflow it.)  Other
+// widths: a bit-field extract, a convert and an FMA per code.
 template <int BITS, int TX>
 __device__ __forceinline__ u4 w_operand(const uint32_t* c, float sc, float bi, int s) {
     float q[8];
     if constexpr (BITS == 4) {
-        uint32_t w = c[s], lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        // the nibble planes as opaque values: otherwise the compiler folds
-        // each mask into a bit-field extract per code, and then converts
-        // byte 0 of it (2 instructions per code instead of the 1 of
-        // v_cvt_f32_ubyte{0..3} on the plane)
-        asm("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            q[2 * e] = (float)((lo >> (8 * e)) & 0xffu);
-            q[2 * e + 1] = (float)((hi >> (8 * e)) & 0xffu);
-        }
+        const float s24 = sc * 0x1p24f, s20 = sc * 0x1p20f;
+        const uint32_t w = c[s], w8 = w >> 8;
+        const uint32_t m0 = w & 0x000F000Fu, m1 = w & 0x00F000F0u;  // codes 0, 4 at p = 0; 1, 5 at p = 4
+        const uint32_t m2 = w8 & 0x000F000Fu, m3 = w8 & 0x00F000F0u;  // codes 2, 6; 3, 7
+        q[0] = fmaf(s24, half_lo(m0), bi); q[4] = fmaf(s24, half_hi(m0), bi);
+        q[1] = fmaf(s20, half_lo(m1), bi); q[5] = fmaf(s20, half_hi(m1), bi);
+        q[2] = fmaf(s24, half_lo(m2), bi); q[6] = fmaf(s24, half_hi(m2), bi);
+        q[3] = fmaf(s20, half_lo(m3), bi); q[7] = fmaf(s20, half_hi(m3), bi);
     } else if constexpr (BITS == 8) {
+        const float s24 = sc * 0x1p24f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) q[e] = (float)((c[2 * s + (e >> 2)] >> (8 * (e & 3))) & 0xffu);
+        for (int h = 0; h < 2; h++) {
+            const uint32_t w = c[2 * s + h];
+            const uint32_t ma = w & 0x00FF00FFu, mb = (w >> 8) & 0x00FF00FFu;  // codes 0, 2; 1, 3
+            q[4 * h] = fmaf(s24, half_lo(ma), bi);     q[4 * h + 2] = fmaf(s24, half_hi(ma), bi);
+            q[4 * h + 1] = fmaf(s24, half_lo(mb), bi); q[4 * h + 3] = fmaf(s24, half_hi(mb), bi);
+        }
+    } else if constexpr (BITS == 3) {
+        // one 24-bit group: codes j and 4 + j at p = 3 j (j = 3 shifted to 0)
+        const float s24 = sc * 0x1p24f, s21 = sc * 0x1p21f, s18 = sc * 0x1p18f;
+        uint32_t g;
+        switch (s) {
+        case 0: g = bits24<0>(c); break;    case 1: g = bits24<24>(c); break;
+        case 2: g = bits24<48>(c); break;   case 3: g = bits24<72>(c); break;
+        case 4: g = bits24<96>(c); break;   case 5: g = bits24<120>(c); break;
+        case 6: g = bits24<144>(c); break;  default: g = bits24<168>(c); break;
+        }
+        const uint32_t t = fold24(g);
+        const uint32_t m0 = t & 0x00070007u, m1 = t & 0x00380038u, m2 = t & 0x01C001C0u, m3 = (t >> 9) & 0x00070007u;
+        q[0] = fmaf(s24, half_lo(m0), bi); q[4] = fmaf(s24, half_hi(m0), bi);
+        q[1] = fmaf(s21, half_lo(m1), bi); q[5] = fmaf(s21, half_hi(m1), bi);
+        q[2] = fmaf(s18, half_lo(m2), bi); q[6] = fmaf(s18, half_hi(m2), bi);
+        q[3] = fmaf(s24, half_lo(m3), bi); q[7] = fmaf(s24, half_hi(m3), bi);
+    } else if constexpr (BITS == 6) {
+        // two 24-bit groups of 4 codes: codes 0, 2 and (shifted) 1, 3 at p = 0
+        const float s24 = sc * 0x1p24f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t g;
+            switch (2 * s + h) {
+            case 0: g = bits24<0>(c); break;     case 1: g = bits24<24>(c); break;
+            case 2: g = bits24<48>(c); break;    case 3: g = bits24<72>(c); break;
+            case 4: g = bits24<96>(c); break;    case 5: g = bits24<120>(c); break;
+            case 6: g = bits24<144>(c); break;   case 7: g = bits24<168>(c); break;
+            case 8: g = bits24<192>(c); break;   case 9: g = bits24<216>(c); break;
+            case 10: g = bits24<240>(c); break;  case 11: g = bits24<264>(c); break;
+            case 12: g = bits24<288>(c); break;  case 13: g = bits24<312>(c); break;
+            case 14: g = bits24<336>(c); break;  default: g = bits24<360>(c); break;
+            }
+            const uint32_t t = fold24(g);
+            const uint32_t ma = t & 0x003F003Fu, mb = (t >> 6) & 0x003F003Fu;
+            q[4 * h] = fmaf(s24, half_lo(ma), bi);     q[4 * h + 2] = fmaf(s24, half_hi(ma), bi);
+            q[4 * h + 1] = fmaf(s24, half_lo(mb), bi); q[4 * h + 3] = fmaf(s24, half_hi(mb), bi);
+        }
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; e++) q[e] = (float)unit_code<BITS>(c, 8 * s + e);
+        for (int e = 0; e < 8; e++) q[e] = fmaf(sc, (float)unit_code<BITS>(c, 8 * s + e), bi);
     }
     u4 r;
-    r.x = pack_t<TX>(fmaf(sc, q[0], bi), fmaf(sc, q[1], bi));
-    r.y = pack_t<TX>(fmaf(sc, q[2], bi), fmaf(sc, q[3], bi));
-    r.z = pack_t<TX>(fmaf(sc, q[4], bi), fmaf(sc, q[5], bi));
-    r.w = pack_t<TX>(fmaf(sc, q[6], bi), fmaf(sc, q[7], bi));
+    r.x = pack_t<TX>(q[0], q[1]);
+    r.y = pack_t<TX>(q[2], q[3]);
+    r.z = pack_t<TX>(q[4], q[5]);
+    r.w = pack_t<TX>(q[6], q[7]);
     return r;
 }
 
