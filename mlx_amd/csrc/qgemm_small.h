@@ -32,6 +32,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWaves = 4;
+constexpr int kCUs = 256;      // compute units of the MI355X
 
 template <int TX>
 __device__ __forceinline__ f32x16 mfma(const u4& a, const u4& b, const f32x16& c) {
@@ -206,18 +207,20 @@ __device__ __forceinline__ int wswz(int r) {
     else return 0;
 }
 
-template <int BITS, int SB, int MT, int GS>
+template <int BITS, int SB, int MT, int NT, int GS>
 struct Lay {
     static constexpr int kSb = SB == DT_F32 ? 4 : 2;
     static constexpr int kXS = MT * 32 * 128;           // one x step
     static constexpr int kRX = MT == 1 ? 3 : 2;         // x steps resident (one being read)
-    static constexpr int kWS = 32 * 32 * BITS;          // one W super-step (4 steps)
+    static constexpr int kWT = 32 * 32 * BITS;          // one column tile's W super-step (4 steps)
+    static constexpr int kWS = NT * kWT;                // a W slot: the NT column tiles
     static constexpr int kSPR = (256 / GS) * kSb;       // scale bytes per row per super-step
     static constexpr int kDpr = kSPR / 4;               // ... in dwords (1..8)
-    static constexpr int kNS = (32 * kDpr + 63) / 64;   // DMAs per scale super-step
-    static constexpr int kSS = 32 * kSPR;
+    static constexpr int kNS = (32 * kDpr + 63) / 64;   // DMAs per column tile's scale super-step
+    static constexpr int kST = 32 * kSPR;
+    static constexpr int kSS = NT * kST;
     static constexpr int kNX = 4 * MT;                  // x DMAs per step
-    static constexpr int kNWS = BITS + 2 * kNS;         // W + scale + bias DMAs per super-step
+    static constexpr int kNWS = NT * (BITS + 2 * kNS);  // W + scale + bias DMAs per super-step
     // loads younger than X(q) when step q waits: the x and W DMAs issued in
     // steps q - kRX + 2 .. q, at most (kRX - 1) x-issues and one W issue
     static constexpr int kMaxWait = (kRX - 1) * kNX + kNWS;
@@ -226,13 +229,13 @@ struct Lay {
     static constexpr int kRW = (4 * kWaveBytes3 <= 160 * 1024) ? 3 : 2;
     static constexpr int kX0 = 0, kW0 = kRX * kXS, kS0 = kW0 + kRW * kWS, kB0 = kS0 + kRW * kSS;
     static constexpr int kWaveBytes = kB0 + kRW * kSS;
-    static constexpr int kRed = 4 * MT * 16 * 64 * 4;   // final K-part reduction (reuses the rings)
+    static constexpr int kRed = 4 * NT * MT * 16 * 64 * 4;  // final K-part reduction (reuses the rings)
     static constexpr int kBytes = (4 * kWaveBytes > kRed) ? 4 * kWaveBytes : kRed;
     static_assert(kMaxWait < 64, "vmcnt holds 6 bits");
     static_assert(kSPR % 4 == 0, "scale rows of a super-step are whole dwords");
 };
 
-template <int BITS, int SB, int MT, int GS>
+template <int BITS, int SB, int MT, int NT, int GS>
 struct Ctx {
     uint32_t lds;                 // LDS address of this wave's rings
     const uint8_t* x;             // x + this wave's first k (bytes)
@@ -240,43 +243,50 @@ struct Ctx {
     const uint8_t* s;             // scales + this wave's first group (bytes)
     const uint8_t* b;
     uint32_t xoff[4 * MT];        // per x DMA: row (clamped) and swizzled chunk
-    uint32_t woff[BITS];          // per W DMA: row (clamped) and chunk
-    uint32_t soff[Lay<BITS, SB, MT, GS>::kNS];
-    bool sact[Lay<BITS, SB, MT, GS>::kNS];
+    uint32_t woff[NT][BITS];      // per column tile and W DMA: row (clamped) and chunk
+    uint32_t soff[NT][Lay<BITS, SB, MT, NT, GS>::kNS];
+    bool sact[Lay<BITS, SB, MT, NT, GS>::kNS];
 };
 
-template <int BITS, int SB, int MT, int GS>
-__device__ __forceinline__ void issue_x(const Ctx<BITS, SB, MT, GS>& c, int qs) {  // qs: step within the part
-    using L = Lay<BITS, SB, MT, GS>;
+template <int BITS, int SB, int MT, int NT, int GS>
+__device__ __forceinline__ void issue_x(const Ctx<BITS, SB, MT, NT, GS>& c, int qs) {  // qs: step within the part
+    using L = Lay<BITS, SB, MT, NT, GS>;
     const uint32_t base = c.lds + L::kX0 + (uint32_t)(qs % L::kRX) * L::kXS;
     const uint8_t* src = c.x + (size_t)qs * 128;
 #pragma unroll
     for (int i = 0; i < L::kNX; i++) dma16(base + 1024u * i, src, c.xoff[i]);
 }
-template <int BITS, int SB, int MT, int GS>
-__device__ __forceinline__ void issue_w(const Ctx<BITS, SB, MT, GS>& c, int u) {  // u: super-step within the part
-    using L = Lay<BITS, SB, MT, GS>;
+template <int BITS, int SB, int MT, int NT, int GS>
+__device__ __forceinline__ void issue_w(const Ctx<BITS, SB, MT, NT, GS>& c, int u) {  // u: super-step within the part
+    using L = Lay<BITS, SB, MT, NT, GS>;
     const uint32_t slot = (uint32_t)(u % L::kRW);
     const uint8_t* src = c.w + (size_t)u * 32 * BITS;
 #pragma unroll
-    for (int i = 0; i < BITS; i++) dma16(c.lds + L::kW0 + slot * L::kWS + 1024u * i, src, c.woff[i]);
+    for (int ct = 0; ct < NT; ct++)
+#pragma unroll
+        for (int i = 0; i < BITS; i++)
+            dma16(c.lds + L::kW0 + slot * L::kWS + ct * L::kWT + 1024u * i, src, c.woff[ct][i]);
     const uint8_t* ss = c.s + (size_t)u * L::kSPR;
     const uint8_t* bs = c.b + (size_t)u * L::kSPR;
 #pragma unroll
-    for (int i = 0; i < L::kNS; i++) {
-        if (c.sact[i]) dma4(c.lds + L::kS0 + slot * L::kSS + 256u * i, ss, c.soff[i]);
-    }
+    for (int ct = 0; ct < NT; ct++)
 #pragma unroll
-    for (int i = 0; i < L::kNS; i++) {
-        if (c.sact[i]) dma4(c.lds + L::kB0 + slot * L::kSS + 256u * i, bs, c.soff[i]);
-    }
+        for (int i = 0; i < L::kNS; i++) {
+            if (c.sact[i]) dma4(c.lds + L::kS0 + slot * L::kSS + ct * L::kST + 256u * i, ss, c.soff[ct][i]);
+        }
+#pragma unroll
+    for (int ct = 0; ct < NT; ct++)
+#pragma unroll
+        for (int i = 0; i < L::kNS; i++) {
+            if (c.sact[i]) dma4(c.lds + L::kB0 + slot * L::kSS + ct * L::kST + 256u * i, bs, c.soff[ct][i]);
+        }
 }
 
 // step q (P = q % 4, compile time) of a wave whose part has nq steps
-template <int BITS, int TX, int SB, int MT, int GS, int P>
-__device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, GS>& c, uint8_t* lw, int q,
+template <int BITS, int TX, int SB, int MT, int NT, int GS, int P>
+__device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, MT, NT, GS>& c, uint8_t* lw, int q,
                                      int nq) {
-    using L = Lay<BITS, SB, MT, GS>;
+    using L = Lay<BITS, SB, MT, NT, GS>;
     const int u = q >> 2;
     // issue: W/scales of super-step u + kRW - 1 (at P == 0), x of step q + kRX - 1
     // (past the part's end they repeat its last super-step / step: counts stay
@@ -306,47 +316,68 @@ __device__ __forceinline__ void step(f32x16 (&acc)[MT], const Ctx<BITS, SB, MT, 
 #pragma unroll
         for (int s = 0; s < 4; s++) xf[t][s] = *reinterpret_cast<const u4*>(xs + r * 128 + (((4 * h + s) ^ swz(r)) * 16));
     }
-    // codes and scale of this lane's 32 codes
+    // codes and scale of this lane's 32 codes in each column tile
     const int slot = u % L::kRW;
-    const uint8_t* wrow = lw + L::kW0 + slot * L::kWS + j * 32 * BITS;
     const int wz = wswz<BITS>(j);
-    uint32_t cw[BITS];
-#pragma unroll
-    for (int i = 0; i < BITS; i++) {
-        const int byte = P * 8 * BITS + 4 * BITS * h + 4 * i;  // within the row, before the swizzle
-        cw[i] = *reinterpret_cast<const uint32_t*>(wrow + ((((byte >> 4) ^ wz) << 4) | (byte & 15)));
-    }
     const int gi = (P * 64 + 32 * h) / GS;
-    const uint8_t* sp = lw + L::kS0 + slot * L::kSS + j * L::kSPR + gi * L::kSb;
-    const uint8_t* bp = lw + L::kB0 + slot * L::kSS + j * L::kSPR + gi * L::kSb;
-    float sc, bi;
-    if constexpr (SB == DT_F32) { sc = *reinterpret_cast<const float*>(sp); bi = *reinterpret_cast<const float*>(bp); }
-    else if constexpr (SB == DT_F16) { sc = f16_to_f32(*reinterpret_cast<const uint16_t*>(sp)); bi = f16_to_f32(*reinterpret_cast<const uint16_t*>(bp)); }
-    else { sc = bf16_to_f32(*reinterpret_cast<const uint16_t*>(sp)); bi = bf16_to_f32(*reinterpret_cast<const uint16_t*>(bp)); }
+    uint32_t cw[NT][BITS];
+    float sc[NT], bi[NT];
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const u4 wop = w_operand<BITS, TX>(cw, sc, bi, s);
+    for (int ct = 0; ct < NT; ct++) {
+        const uint8_t* wrow = lw + L::kW0 + slot * L::kWS + ct * L::kWT + j * 32 * BITS;
 #pragma unroll
-        for (int t = 0; t < MT; t++) acc[t] = mfma<TX>(xf[t][s], wop, acc[t]);
+        for (int i = 0; i < BITS; i++) {
+            const int byte = P * 8 * BITS + 4 * BITS * h + 4 * i;  // within the row, before the swizzle
+            cw[ct][i] = *reinterpret_cast<const uint32_t*>(wrow + ((((byte >> 4) ^ wz) << 4) | (byte & 15)));
+        }
+        const uint8_t* sp = lw + L::kS0 + slot * L::kSS + ct * L::kST + j * L::kSPR + gi * L::kSb;
+        const uint8_t* bp = lw + L::kB0 + slot * L::kSS + ct * L::kST + j * L::kSPR + gi * L::kSb;
+        if constexpr (SB == DT_F32) {
+            sc[ct] = *reinterpret_cast<const float*>(sp);
+            bi[ct] = *reinterpret_cast<const float*>(bp);
+        } else if constexpr (SB == DT_F16) {
+            sc[ct] = f16_to_f32(*reinterpret_cast<const uint16_t*>(sp));
+            bi[ct] = f16_to_f32(*reinterpret_cast<const uint16_t*>(bp));
+        } else {
+            sc[ct] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(sp));
+            bi[ct] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(bp));
+        }
     }
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int ct = 0; ct < NT; ct++) {
+            const u4 wop = w_operand<BITS, TX>(cw[ct], sc[ct], bi[ct], s);
+#pragma unroll
+            for (int t = 0; t < MT; t++) acc[ct][t] = mfma<TX>(xf[t][s], wop, acc[ct][t]);
+        }
 }
 
-template <int BITS, int TX, int SB, int MT, int GS, bool EPI>
+// NT column tiles of 32 per block.  One block per CU (the rings take most
+// of the LDS), and a block's time is set by its waves' own instruction
+// stream (dequant VALU and MFMA, one wave per SIMD), hardly by how many
+// blocks run beside it: a round of 64 blocks and one of 256 take about the
+// same time (M = 64, K = 4096, one tile: 12.2 / 13.4 us), and a second,
+// partial round costs a whole one (288 blocks: 23.0 us).  Two tiles per block
+// double a block's work but halve the block count and x's re-reads: slower
+// when one round of one-tile blocks covers N, faster when it takes two (the
+// launcher picks).
+template <int BITS, int TX, int SB, int MT, int NT, int GS, bool EPI>
 __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep) {
-    using L = Lay<BITS, SB, MT, GS>;
+    using L = Lay<BITS, SB, MT, NT, GS>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 31, h = lane >> 5;
-    const int n0 = blockIdx.x * 32;
+    const int n0 = blockIdx.x * 32 * NT;
     const int G = K / GS;
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int nq = K / 64 / kWaves;        // steps of this wave's K part (a multiple of 4)
     const int k0 = wave * nq * 64;         // first k of the part
 
-    Ctx<BITS, SB, MT, GS> c;
+    Ctx<BITS, SB, MT, NT, GS> c;
     c.lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds) + (uint32_t)wave * L::kWaveBytes;
     c.x = static_cast<const uint8_t*>(x) + (size_t)k0 * 2;
     c.w = reinterpret_cast<const uint8_t*>(wq) + (size_t)k0 * BITS / 8;
@@ -360,17 +391,20 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
         c.xoff[i] = ((uint32_t)m * K + 8 * chunk) * 2;
     }
 #pragma unroll
-    for (int i = 0; i < BITS; i++) {
-        const int v = 64 * i + lane, r = v / (2 * BITS), ch = v % (2 * BITS);
-        const int n = n0 + r < N ? n0 + r : N - 1;
-        c.woff[i] = (uint32_t)n * row_bytes + 16u * (ch ^ wswz<BITS>(r));  // lands at position ch
-    }
+    for (int ct = 0; ct < NT; ct++) {
 #pragma unroll
-    for (int i = 0; i < L::kNS; i++) {
-        const int v = 64 * i + lane, r = v / L::kDpr, d = v % L::kDpr;
-        const int n = n0 + r < N ? n0 + r : N - 1;
-        c.sact[i] = v < 32 * L::kDpr;
-        c.soff[i] = (uint32_t)n * G * L::kSb + 4u * d;
+        for (int i = 0; i < BITS; i++) {
+            const int v = 64 * i + lane, r = v / (2 * BITS), ch = v % (2 * BITS);
+            const int n = n0 + 32 * ct + r < N ? n0 + 32 * ct + r : N - 1;
+            c.woff[ct][i] = (uint32_t)n * row_bytes + 16u * (ch ^ wswz<BITS>(r));  // lands at position ch
+        }
+#pragma unroll
+        for (int i = 0; i < L::kNS; i++) {
+            const int v = 64 * i + lane, r = v / L::kDpr, d = v % L::kDpr;
+            const int n = n0 + 32 * ct + r < N ? n0 + 32 * ct + r : N - 1;
+            c.sact[i] = v < 32 * L::kDpr;
+            c.soff[ct][i] = (uint32_t)n * G * L::kSb + 4u * d;
+        }
     }
     uint8_t* lw = lds + (size_t)wave * L::kWaveBytes;
 
@@ -382,40 +416,118 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     for (int qq = 0; qq < L::kRX - 1; qq++) issue_x(c, qq < nq - 1 ? qq : nq - 1);
     // the steady state's W issue of super-step kRW - 1 happens in step 0
 
-    f32x16 acc[MT];
+    f32x16 acc[NT][MT];
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int ct = 0; ct < NT; ct++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[ct][t][v] = 0.f;
     for (int q = 0; q < nq; q += 4) {
-        step<BITS, TX, SB, MT, GS, 0>(acc, c, lw, q, nq);
-        step<BITS, TX, SB, MT, GS, 1>(acc, c, lw, q + 1, nq);
-        step<BITS, TX, SB, MT, GS, 2>(acc, c, lw, q + 2, nq);
-        step<BITS, TX, SB, MT, GS, 3>(acc, c, lw, q + 3, nq);
+        step<BITS, TX, SB, MT, NT, GS, 0>(acc, c, lw, q, nq);
+        step<BITS, TX, SB, MT, NT, GS, 1>(acc, c, lw, q + 1, nq);
+        step<BITS, TX, SB, MT, NT, GS, 2>(acc, c, lw, q + 2, nq);
+        step<BITS, TX, SB, MT, NT, GS, 3>(acc, c, lw, q + 3, nq);
     }
     wait_vmcnt_small<0>();
     __syncthreads();
 
     // ---- the four K parts meet in LDS; wave w stores accumulator VGPRs 4w..4w+3 ----
-    float* red = reinterpret_cast<float*>(lds);   // [wave][MT*16][64]
+    constexpr int kAcc = NT * MT * 16;            // accumulator VGPRs per lane
+    float* red = reinterpret_cast<float*>(lds);   // [wave][kAcc][64]
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int ct = 0; ct < NT; ct++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) red[((size_t)wave * MT * 16 + t * 16 + v) * 64 + lane] = acc[t][v];
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                red[((size_t)wave * kAcc + (ct * MT + t) * 16 + v) * 64 + lane] = acc[ct][t][v];
     __syncthreads();
-    const int nn = n0 + j;
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int ct = 0; ct < NT; ct++) {
+        const int nn = n0 + 32 * ct + j;
 #pragma unroll
-        for (int vv = 0; vv < 4; vv++) {
-            const int v = 4 * wave + vv;
-            float sum = 0.f;
+        for (int t = 0; t < MT; t++)
 #pragma unroll
-            for (int w2 = 0; w2 < kWaves; w2++) sum += red[((size_t)w2 * MT * 16 + t * 16 + v) * 64 + lane];
-            // 32x32 accumulator layout: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
-            const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (m < M && nn < N) store_out<EPI>(y, (size_t)m * N + nn, nn, ep, sum);
-        }
+            for (int vv = 0; vv < 4; vv++) {
+                const int v = 4 * wave + vv;
+                float sum = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < kWaves; w2++)
+                    sum += red[((size_t)w2 * kAcc + (ct * MT + t) * 16 + v) * 64 + lane];
+                // 32x32 accumulator layout: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
+                const int m = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (m < M && nn < N) store_out<EPI>(y, (size_t)m * N + nn, nn, ep, sum);
+            }
+    }
+}
+
+// whether two column tiles per block fit: both tiles' W rings beside x's
+template <int BITS, int SB, int MT, int GS>
+constexpr bool small_nt2_fits() {
+    return 4 * Lay<BITS, SB, MT, 2, GS>::kWaveBytes <= 160 * 1024;
+}
+
+template <int BITS, int TX, int SB, int MT, int NT, int GS, bool EPI>
+LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
+    using L = Lay<BITS, SB, MT, NT, GS>;
+    static_assert(L::kBytes <= 160 * 1024, "LDS");
+    auto kern = qgemm_small_kernel<BITS, TX, SB, MT, NT, GS, EPI>;
+    // once per instantiation; a function-local static initializes exactly once
+    // even when several threads make the first call together
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+    if (attr != hipSuccess) return LuxStatus::Internal;
+    hipLaunchKernelGGL(kern, dim3((a.N + 32 * NT - 1) / (32 * NT)), dim3(64 * kWaves), L::kBytes, st, a.x, a.wq,
+                       a.scales, a.biases, a.y, a.M, a.K, a.N, a.epi());
+    return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
+}
+
+template <int BITS, int TX, int SB, int MT, int NT, int GS>
+LuxStatus launch_nt(const QmmArgs& a, hipStream_t st) {
+    return a.has_epilogue() ? launch_e<BITS, TX, SB, MT, NT, GS, true>(a, st)
+                            : launch_e<BITS, TX, SB, MT, NT, GS, false>(a, st);
+}
+
+// two tiles per block where one-tile blocks would need a second round on the
+// kCUs CUs (M = 64, K = 4096, 4-bit: N = 11008 17.3 us against 22.6, N =
+// 16384 22.8 against 26.9; N = 8192 16.0 against 13.1 stays one tile)
+template <int BITS, int TX, int SB, int MT, int GS>
+LuxStatus launch(const QmmArgs& a, hipStream_t st) {
+    if constexpr (small_nt2_fits<BITS, SB, MT, GS>()) {
+        if ((a.N + 31) / 32 > kCUs) return launch_nt<BITS, TX, SB, MT, 2, GS>(a, st);
+    }
+    return launch_nt<BITS, TX, SB, MT, 1, GS>(a, st);
+}
+
+template <int BITS, int TX, int SB, int MT>
+LuxStatus launch_gs(const QmmArgs& a, hipStream_t st) {
+    switch (a.group_size) {
+    case 32: return launch<BITS, TX, SB, MT, 32>(a, st);
+    case 64: return launch<BITS, TX, SB, MT, 64>(a, st);
+    default: return launch<BITS, TX, SB, MT, 128>(a, st);
+    }
+}
+
+template <int BITS, int TX, int SB>
+LuxStatus launch_mt(const QmmArgs& a, hipStream_t st) {
+    return a.M <= 32 ? launch_gs<BITS, TX, SB, 1>(a, st) : launch_gs<BITS, TX, SB, 2>(a, st);
+}
+
+template <int BITS, int TX>
+LuxStatus launch_sb(const QmmArgs& a, hipStream_t st) {
+    switch (a.sb_dtype) {
+    case DT_F32: return launch_mt<BITS, TX, DT_F32>(a, st);
+    case DT_F16: return launch_mt<BITS, TX, DT_F16>(a, st);
+    default: return launch_mt<BITS, TX, DT_BF16>(a, st);
+    }
+}
+
+// one explicit instantiation per code width, each in its own translation
+// unit (qgemm_small_b{2,3,4,5,6,8}.hip)
+template <int BITS>
+LuxStatus launch_tx(const QmmArgs& a, hipStream_t st) {
+    return a.x_dtype == DT_F16 ? launch_sb<BITS, DT_F16>(a, st) : launch_sb<BITS, DT_BF16>(a, st);
 }
 
 }  // namespace small

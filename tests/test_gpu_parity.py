@@ -450,6 +450,22 @@ def test_small_gemm_parity(ctx, oracle, bits, xd, sbd, od):
 
 
 @pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, F32, F32)])
+def test_small_gemm_two_tiles_parity(ctx, oracle, bits, xd, sbd, od):
+    """Past 256 column tiles of 32 (N > 8192) the small-M GEMM runs two tiles
+    per block where their rings fit (2- to 5-bit codes; 6/8-bit blocks keep
+    one tile and run two rounds): ragged N with the last block's second tile
+    wholly past N (N = 8200), group sizes 32 (f32 scales at 32: the rings
+    fill the 160 KB exactly), 64 and 128, one and two M tiles."""
+    O = oracle
+    for (M, K, N, gs) in [(64, 1024, 8200, 32), (17, 2048, 9000, 64), (40, 1024, 12345, 128)]:
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 7 + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, variant="omp", w_round=xd)
+        check_output(O, y, want, od, f"small gemm two tiles b{bits} M{M} K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_split_k_gemm_parity(ctx, oracle, bits, xd, sbd, od):
     """8 < M <= 64 with K % 128 == 0 and K % 1024 != 0: the split-K small-M
