@@ -637,6 +637,7 @@ FUSED_CASES = [
     (6, 4096, 64, 4, 64, BF16),     # decode MFMA kernel
     (6, 2048, 40, 8, 128, F16),     # mid-M ring kernel (8-bit)
     (32, 2048, 72, 4, 64, BF16),    # small-M GEMM
+    (24, 1024, 8300, 3, 64, F16),   # small-M GEMM, two column tiles per block (N > 8192)
     (40, 2560, 200, 4, 64, F16),    # split-K small-M GEMM (10 K parts)
     (96, 512, 136, 4, 64, F16),     # large GEMM
     (3, 96, 20, 4, 32, F32),        # generic kernel (K % 64 != 0)
