@@ -354,14 +354,13 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
 }
 
 // NT column tiles of 32 per block.  One block per CU (the rings take most
-// of the LDS), and a block's time is set by its waves' own instruction
-// stream (dequant VALU and MFMA, one wave per SIMD), hardly by how many
-// blocks run beside it: a round of 64 blocks and one of 256 take about the
-// same time (M = 64, K = 4096, one tile: 12.2 / 13.4 us), and a second,
-// partial round costs a whole one (288 blocks: 23.0 us).  Two tiles per block
-// double a block's work but halve the block count and x's re-reads: slower
-// when one round of one-tile blocks covers N, faster when it takes two (the
-// launcher picks).
+// of the LDS), and a block's time hardly depends on how many blocks run
+// beside it: a round of 64 blocks and one of 256 take about the same time
+// (M = 64, K = 4096, one tile: 12.2 / 13.4 us), and a second, partial round
+// costs a whole one (288 blocks: 23.0 us).  Two tiles per block double a
+// block's dequant and MFMA work but halve the block count and x's
+// re-reads: slower when one round of one-tile blocks covers N, faster when
+// it takes two (the launcher picks).
 template <int BITS, int TX, int SB, int MT, int NT, int GS, bool EPI>
 __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
