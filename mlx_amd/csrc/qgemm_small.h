@@ -212,27 +212,39 @@ struct Lay {
     static constexpr int kSb = SB == DT_F32 ? 4 : 2;
     static constexpr int kXS = MT * 32 * 128;           // one x step
     static constexpr int kRX = MT == 1 ? 3 : 2;         // x steps resident (one being read)
-    static constexpr int kWT = 32 * 32 * BITS;          // one column tile's W super-step (4 steps)
-    static constexpr int kWS = NT * kWT;                // a W slot: the NT column tiles
     static constexpr int kSPR = (256 / GS) * kSb;       // scale bytes per row per super-step
     static constexpr int kDpr = kSPR / 4;               // ... in dwords (1..8)
     static constexpr int kNS = (32 * kDpr + 63) / 64;   // DMAs per column tile's scale super-step
     static constexpr int kST = 32 * kSPR;
     static constexpr int kSS = NT * kST;
     static constexpr int kNX = 4 * MT;                  // x DMAs per step
-    static constexpr int kNWS = NT * (BITS + 2 * kNS);  // W + scale + bias DMAs per super-step
+    // Half W slots (kHW: two 6-bit tiles, whose whole-super-step W slots do
+    // not fit twice beside x's): W in a ring of three slots of two steps
+    // each, one refilled every two steps (steps 0 and 2 of a super-step), 4
+    // steps ahead as with two whole slots; scales keep two super-step slots
+    static constexpr bool kHW =
+        NT == 2 && MT == 2 && BITS == 6 && 4 * (kRX * kXS + 2 * (NT * 32 * 32 * BITS + 2 * kSS)) > 160 * 1024;
+    static constexpr int kWRow = kHW ? 16 * BITS : 32 * BITS;  // W bytes of a row in a slot
+    static constexpr int kWT = 32 * kWRow;              // one column tile's W slot
+    static constexpr int kWS = NT * kWT;                // a W slot: the NT column tiles
+    static constexpr int kNWI = kHW ? BITS / 2 : BITS;  // W DMAs per column tile and W issue
+    static constexpr int kNSS = 2 * NT * kNS;           // scale + bias DMAs per super-step
+    static constexpr int kNWS = NT * kNWI + kNSS;       // DMAs of the largest W issue
     // loads younger than X(q) when step q waits: the x and W DMAs issued in
     // steps q - kRX + 2 .. q, at most (kRX - 1) x-issues and one W issue
     static constexpr int kMaxWait = (kRX - 1) * kNX + kNWS;
     // W super-steps resident: 3 (two in flight) unless LDS or vmcnt say 2
     static constexpr int kWaveBytes3 = kRX * kXS + 3 * (kWS + 2 * kSS);
-    static constexpr int kRW = (4 * kWaveBytes3 <= 160 * 1024) ? 3 : 2;
-    static constexpr int kX0 = 0, kW0 = kRX * kXS, kS0 = kW0 + kRW * kWS, kB0 = kS0 + kRW * kSS;
+    static constexpr int kRW = (!kHW && 4 * kWaveBytes3 <= 160 * 1024) ? 3 : 2;  // scale slots (and W slots unless kHW)
+    static constexpr int kRWW = kHW ? 3 : kRW;          // W slots
+    static constexpr int kX0 = 0, kW0 = kRX * kXS, kS0 = kW0 + kRWW * kWS, kB0 = kS0 + kRW * kSS;
     static constexpr int kWaveBytes = kB0 + kRW * kSS;
     static constexpr int kRed = 4 * NT * MT * 16 * 64 * 4;  // final K-part reduction (reuses the rings)
     static constexpr int kBytes = (4 * kWaveBytes > kRed) ? 4 * kWaveBytes : kRed;
     static_assert(kMaxWait < 64, "vmcnt holds 6 bits");
     static_assert(kSPR % 4 == 0, "scale rows of a super-step are whole dwords");
+    static_assert(!kHW || (BITS % 2 == 0 && (2 * BITS & (2 * BITS - 1)) != 0),
+                  "half slots: whole DMAs per half, rows not chunk-swizzled");
 };
 
 template <int BITS, int SB, int MT, int NT, int GS>
@@ -256,16 +268,31 @@ __device__ __forceinline__ void issue_x(const Ctx<BITS, SB, MT, NT, GS>& c, int 
 #pragma unroll
     for (int i = 0; i < L::kNX; i++) dma16(base + 1024u * i, src, c.xoff[i]);
 }
+// half-slot W (kHW): half hh (steps 2 hh, 2 hh + 1 of the part) into slot hh % 3
+template <int BITS, int SB, int MT, int NT, int GS>
+__device__ __forceinline__ void issue_wh(const Ctx<BITS, SB, MT, NT, GS>& c, int hh) {
+    using L = Lay<BITS, SB, MT, NT, GS>;
+    const uint32_t slot = (uint32_t)(hh % 3);
+    const uint8_t* src = c.w + (size_t)hh * 16 * BITS;
+#pragma unroll
+    for (int ct = 0; ct < NT; ct++)
+#pragma unroll
+        for (int i = 0; i < L::kNWI; i++)
+            dma16(c.lds + L::kW0 + slot * L::kWS + ct * L::kWT + 1024u * i, src, c.woff[ct][i]);
+}
+// W (unless kHW) and the scales and biases of super-step u into slot u % kRW
 template <int BITS, int SB, int MT, int NT, int GS>
 __device__ __forceinline__ void issue_w(const Ctx<BITS, SB, MT, NT, GS>& c, int u) {  // u: super-step within the part
     using L = Lay<BITS, SB, MT, NT, GS>;
     const uint32_t slot = (uint32_t)(u % L::kRW);
-    const uint8_t* src = c.w + (size_t)u * 32 * BITS;
+    if constexpr (!L::kHW) {
+        const uint8_t* src = c.w + (size_t)u * 32 * BITS;
 #pragma unroll
-    for (int ct = 0; ct < NT; ct++)
+        for (int ct = 0; ct < NT; ct++)
 #pragma unroll
-        for (int i = 0; i < BITS; i++)
-            dma16(c.lds + L::kW0 + slot * L::kWS + ct * L::kWT + 1024u * i, src, c.woff[ct][i]);
+            for (int i = 0; i < BITS; i++)
+                dma16(c.lds + L::kW0 + slot * L::kWS + ct * L::kWT + 1024u * i, src, c.woff[ct][i]);
+    }
     const uint8_t* ss = c.s + (size_t)u * L::kSPR;
     const uint8_t* bs = c.b + (size_t)u * L::kSPR;
 #pragma unroll
@@ -292,7 +319,18 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     // (past the part's end they repeat its last super-step / step: counts stay
     // fixed), once the previous step's reads of the refilled slots are done
     wait_lds_reads();
-    if constexpr (P == 0) {
+    if constexpr (L::kHW) {
+        // half 2 (u + P / 2) + 2 into the slot half - 1 used, at P == 0 also
+        // the scales of super-step u + 1
+        if constexpr (P == 0 || P == 2) {
+            const int hw = 2 * u + P / 2 + 2, hl = 2 * (nq >> 2) - 1;
+            issue_wh(c, hw < hl ? hw : hl);
+        }
+        if constexpr (P == 0) {
+            const int uw = u + 1, ul = (nq >> 2) - 1;
+            issue_w(c, uw < ul ? uw : ul);
+        }
+    } else if constexpr (P == 0) {
         const int uw = u + L::kRW - 1, ul = (nq >> 2) - 1;
         issue_w(c, uw < ul ? uw : ul);
     }
@@ -303,8 +341,10 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     // X(q) (and the older W(u)) landed: younger are the issues of steps
     // q - kRX + 2 .. q: kRX - 1 x issues, plus the W issue of the one of
     // those steps that starts a super-step, if any (P <= kRX - 2; kRX <= 5)
-    static_assert(L::kRX >= 2 && L::kRX <= 5, "one W issue at most among the younger steps");
-    constexpr int kYoung = (L::kRX - 1) * L::kNX + L::kNWS * (P <= L::kRX - 2 ? 1 : 0);
+    static_assert(L::kRX >= 2 && L::kRX <= (L::kHW ? 2 : 5), "one W issue at most among the younger steps");
+    constexpr int kYoung = (L::kRX - 1) * L::kNX +
+                           (L::kHW ? (P == 0 ? L::kNWS : P == 2 ? NT * L::kNWI : 0)
+                                   : L::kNWS * (P <= L::kRX - 2 ? 1 : 0));
     wait_vmcnt_small<kYoung>();
     const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
     // x fragments
@@ -318,16 +358,18 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     }
     // codes and scale of this lane's 32 codes in each column tile
     const int slot = u % L::kRW;
+    const int wslot = L::kHW ? (2 * u + P / 2) % 3 : slot;
     const int wz = wswz<BITS>(j);
     const int gi = (P * 64 + 32 * h) / GS;
     uint32_t cw[NT][BITS];
     float sc[NT], bi[NT];
 #pragma unroll
     for (int ct = 0; ct < NT; ct++) {
-        const uint8_t* wrow = lw + L::kW0 + slot * L::kWS + ct * L::kWT + j * 32 * BITS;
+        const uint8_t* wrow = lw + L::kW0 + wslot * L::kWS + ct * L::kWT + j * L::kWRow;
 #pragma unroll
         for (int i = 0; i < BITS; i++) {
-            const int byte = P * 8 * BITS + 4 * BITS * h + 4 * i;  // within the row, before the swizzle
+            // within the row, before the swizzle (a half slot holds steps 2 (P / 2), + 1)
+            const int byte = (L::kHW ? P & 1 : P) * 8 * BITS + 4 * BITS * h + 4 * i;
             cw[ct][i] = *reinterpret_cast<const uint32_t*>(wrow + ((((byte >> 4) ^ wz) << 4) | (byte & 15)));
         }
         const uint8_t* sp = lw + L::kS0 + slot * L::kSS + ct * L::kST + j * L::kSPR + gi * L::kSb;
@@ -392,8 +434,9 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
 #pragma unroll
     for (int ct = 0; ct < NT; ct++) {
 #pragma unroll
-        for (int i = 0; i < BITS; i++) {
-            const int v = 64 * i + lane, r = v / (2 * BITS), ch = v % (2 * BITS);
+        for (int i = 0; i < L::kNWI; i++) {
+            constexpr int kCpr = L::kWRow / 16;                   // 16-byte chunks of a row in a slot
+            const int v = 64 * i + lane, r = v / kCpr, ch = v % kCpr;
             const int n = n0 + 32 * ct + r < N ? n0 + 32 * ct + r : N - 1;
             c.woff[ct][i] = (uint32_t)n * row_bytes + 16u * (ch ^ wswz<BITS>(r));  // lands at position ch
         }
@@ -409,6 +452,10 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
 
     // prologue: the issues of steps -kRX+1 .. -1 and super-steps up to kRW - 2
     // in the same order the steady state keeps (missing ones repeat step 0)
+    if constexpr (L::kHW) {
+        issue_wh(c, 0);
+        issue_wh(c, 1);                    // a part has at least one super-step: two halves
+    }
 #pragma unroll
     for (int uu = 0; uu < L::kRW - 1; uu++) issue_w(c, uu < (nq >> 2) - 1 ? uu : (nq >> 2) - 1);
 #pragma unroll
