@@ -512,7 +512,9 @@ def test_split_k_shapes_in_sequence(ctx, oracle):
 
 @pytest.mark.parametrize("M,K,N,bits,gs,xd,kern", [
     (32, 8192, 8192, 8, 128, BF16, "gemm"),   # small-M GEMM, one block per CU
-    (64, 4096, 11008, 3, 64, F16, "gemm"),    # two M tiles, ragged grid
+    (64, 4096, 11008, 3, 64, F16, "gemm"),    # two M tiles, two column tiles per block, ragged grid
+    (64, 4096, 11008, 6, 64, F16, "gemm"),    # the same with the 6-bit half-slot W ring
+    (32, 8192, 16384, 4, 64, BF16, "gemm"),   # one M tile, two column tiles per block, 256 blocks
     (16, 4096, 14336, 4, 64, BF16, "gemv"),   # mid-M GEMV rings
 ])
 def test_ring_kernels_repeat_full_grid(ctx, oracle, M, K, N, bits, gs, xd, kern):
