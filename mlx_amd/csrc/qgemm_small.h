@@ -192,17 +192,16 @@ __device__ __forceinline__ void dma4(uint32_t m0v, const void* sbase, uint32_t v
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// W rows of a super-step slot are 32*BITS bytes = 2*BITS 16-byte chunks.
-// Where that count is a power of two (BITS 2, 4, 8) chunk c of row r sits at
-// position c ^ wswz(r) (through the DMA source address, like x): the row
-// stride is a multiple of 64 B (256 B for 8-bit codes, a whole bank cycle),
-// so without it the 32 lanes reading 32 rows' codes hit the same banks
-// (measured at c2: 3.9M conflict cycles against 0.3M active LDS cycles).
-// 16 consecutive rows reading one chunk then cover 16 distinct 16-byte slots
-// of a 256-byte bank window.
-template <int BITS>
+// W rows of a super-step slot are 32*BITS bytes = 2*BITS 16-byte chunks
+// (half that in a half slot).  Where that count kCpr is a power of two
+// (BITS 2, 4, 8) chunk c of row r sits at position c ^ wswz(r) (through the
+// DMA source address, like x): the row stride is a multiple of 64 B (256 B
+// for 8-bit codes, a whole bank cycle), so without it the 32 lanes reading
+// 32 rows' codes hit the same banks (measured at c2: 3.9M conflict cycles
+// against 0.3M active LDS cycles).  16 consecutive rows reading one chunk
+// then cover 16 distinct 16-byte slots of a 256-byte bank window.
+template <int kCpr>
 __device__ __forceinline__ int wswz(int r) {
-    constexpr int kCpr = 2 * BITS;
     if constexpr ((kCpr & (kCpr - 1)) == 0 && kCpr <= 16) return (r / (16 / kCpr)) & (kCpr - 1);
     else return 0;
 }
@@ -218,12 +217,12 @@ struct Lay {
     static constexpr int kST = 32 * kSPR;
     static constexpr int kSS = NT * kST;
     static constexpr int kNX = 4 * MT;                  // x DMAs per step
-    // Half W slots (kHW: two 6-bit tiles, whose whole-super-step W slots do
-    // not fit twice beside x's): W in a ring of three slots of two steps
+    // Half W slots (kHW: two 6- or 8-bit tiles, whose whole-super-step W
+    // slots do not fit twice beside x's): W in a ring of three slots of two steps
     // each, one refilled every two steps (steps 0 and 2 of a super-step), 4
     // steps ahead as with two whole slots; scales keep two super-step slots
-    static constexpr bool kHW =
-        NT == 2 && MT == 2 && BITS == 6 && 4 * (kRX * kXS + 2 * (NT * 32 * 32 * BITS + 2 * kSS)) > 160 * 1024;
+    static constexpr bool kHW = NT == 2 && (BITS == 6 || BITS == 8) &&
+                                4 * (kRX * kXS + 2 * (NT * 32 * 32 * BITS + 2 * kSS)) > 160 * 1024;
     static constexpr int kWRow = kHW ? 16 * BITS : 32 * BITS;  // W bytes of a row in a slot
     static constexpr int kWT = 32 * kWRow;              // one column tile's W slot
     static constexpr int kWS = NT * kWT;                // a W slot: the NT column tiles
@@ -243,8 +242,7 @@ struct Lay {
     static constexpr int kBytes = (4 * kWaveBytes > kRed) ? 4 * kWaveBytes : kRed;
     static_assert(kMaxWait < 64, "vmcnt holds 6 bits");
     static_assert(kSPR % 4 == 0, "scale rows of a super-step are whole dwords");
-    static_assert(!kHW || (BITS % 2 == 0 && (2 * BITS & (2 * BITS - 1)) != 0),
-                  "half slots: whole DMAs per half, rows not chunk-swizzled");
+    static_assert(!kHW || BITS % 2 == 0, "half slots: whole DMAs per half");
 };
 
 template <int BITS, int SB, int MT, int NT, int GS>
@@ -341,9 +339,12 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     // X(q) (and the older W(u)) landed: younger are the issues of steps
     // q - kRX + 2 .. q: kRX - 1 x issues, plus the W issue of the one of
     // those steps that starts a super-step, if any (P <= kRX - 2; kRX <= 5)
-    static_assert(L::kRX >= 2 && L::kRX <= (L::kHW ? 2 : 5), "one W issue at most among the younger steps");
+    static_assert(L::kRX >= 2 && L::kRX <= (L::kHW ? 3 : 5), "one W issue at most among the younger steps");
+    // kHW: the W halves issued at the even steps among q - kRX + 2 .. q, the
+    // scales at the step among them that starts a super-step
     constexpr int kYoung = (L::kRX - 1) * L::kNX +
-                           (L::kHW ? (P == 0 ? L::kNWS : P == 2 ? NT * L::kNWI : 0)
+                           (L::kHW ? (P % 2 == 0 || L::kRX == 3 ? NT * L::kNWI : 0) +
+                                         (P <= L::kRX - 2 ? L::kNSS : 0)
                                    : L::kNWS * (P <= L::kRX - 2 ? 1 : 0));
     wait_vmcnt_small<kYoung>();
     const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
@@ -359,7 +360,7 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     // codes and scale of this lane's 32 codes in each column tile
     const int slot = u % L::kRW;
     const int wslot = L::kHW ? (2 * u + P / 2) % 3 : slot;
-    const int wz = wswz<BITS>(j);
+    const int wz = wswz<L::kWRow / 16>(j);
     const int gi = (P * 64 + 32 * h) / GS;
     uint32_t cw[NT][BITS];
     float sc[NT], bi[NT];
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
             constexpr int kCpr = L::kWRow / 16;                   // 16-byte chunks of a row in a slot
             const int v = 64 * i + lane, r = v / kCpr, ch = v % kCpr;
             const int n = n0 + 32 * ct + r < N ? n0 + 32 * ct + r : N - 1;
-            c.woff[ct][i] = (uint32_t)n * row_bytes + 16u * (ch ^ wswz<BITS>(r));  // lands at position ch
+            c.woff[ct][i] = (uint32_t)n * row_bytes + 16u * (ch ^ wswz<kCpr>(r));  // lands at position ch
         }
 #pragma unroll
         for (int i = 0; i < L::kNS; i++) {
