@@ -217,32 +217,39 @@ struct Lay {
     static constexpr int kST = 32 * kSPR;
     static constexpr int kSS = NT * kST;
     static constexpr int kNX = 4 * MT;                  // x DMAs per step
-    // Half W slots (kHW: two 6- or 8-bit tiles, whose whole-super-step W
-    // slots do not fit twice beside x's): W in a ring of three slots of two steps
-    // each, one refilled every two steps (steps 0 and 2 of a super-step), 4
-    // steps ahead as with two whole slots; scales keep two super-step slots
-    static constexpr bool kHW = NT == 2 && (BITS == 6 || BITS == 8) &&
-                                4 * (kRX * kXS + 2 * (NT * 32 * 32 * BITS + 2 * kSS)) > 160 * 1024;
-    static constexpr int kWRow = kHW ? 16 * BITS : 32 * BITS;  // W bytes of a row in a slot
+    // Part-super-step W slots (two 6- or 8-bit tiles, whose whole-super-step
+    // W slots do not fit twice beside x's): W in a ring of kRWW slots of kSW
+    // steps, half (3 slots of 2 steps) or, where that does not fit either,
+    // quarter (5 slots of one step) super-steps, one refilled every kSW
+    // steps and 4 steps ahead as with two whole slots; scales keep two
+    // super-step slots
+    static constexpr int kFull = kRX * kXS + 2 * (NT * 32 * 32 * BITS + 2 * kSS);
+    static constexpr int kHalf = kRX * kXS + 3 * (NT * 32 * 16 * BITS) + 2 * 2 * kSS;
+    static constexpr int kSW = NT != 2 || (BITS != 6 && BITS != 8) || 4 * kFull <= 160 * 1024 ? 4
+                               : 4 * kHalf <= 160 * 1024 || BITS != 8                          ? 2
+                                                                                               : 1;
+    static constexpr bool kHW = kSW < 4;
+    static constexpr int kWRow = 8 * BITS * kSW;        // W bytes of a row in a slot
     static constexpr int kWT = 32 * kWRow;              // one column tile's W slot
     static constexpr int kWS = NT * kWT;                // a W slot: the NT column tiles
-    static constexpr int kNWI = kHW ? BITS / 2 : BITS;  // W DMAs per column tile and W issue
+    static constexpr int kNWI = BITS * kSW / 4;         // W DMAs per column tile and W issue
     static constexpr int kNSS = 2 * NT * kNS;           // scale + bias DMAs per super-step
     static constexpr int kNWS = NT * kNWI + kNSS;       // DMAs of the largest W issue
     // loads younger than X(q) when step q waits: the x and W DMAs issued in
     // steps q - kRX + 2 .. q, at most (kRX - 1) x-issues and one W issue
-    static constexpr int kMaxWait = (kRX - 1) * kNX + kNWS;
+    static constexpr int kMaxWait = (kRX - 1) * (kNX + NT * kNWI) + kNSS;
     // W super-steps resident: 3 (two in flight) unless LDS or vmcnt say 2
     static constexpr int kWaveBytes3 = kRX * kXS + 3 * (kWS + 2 * kSS);
     static constexpr int kRW = (!kHW && 4 * kWaveBytes3 <= 160 * 1024) ? 3 : 2;  // scale slots (and W slots unless kHW)
-    static constexpr int kRWW = kHW ? 3 : kRW;          // W slots
+    static constexpr int kRWW = kSW == 4 ? kRW : kSW == 2 ? 3 : 5;  // W slots
+    static constexpr int kLead = kRWW - 1;              // part-super-step slots issued ahead
     static constexpr int kX0 = 0, kW0 = kRX * kXS, kS0 = kW0 + kRWW * kWS, kB0 = kS0 + kRW * kSS;
     static constexpr int kWaveBytes = kB0 + kRW * kSS;
     static constexpr int kRed = 4 * NT * MT * 16 * 64 * 4;  // final K-part reduction (reuses the rings)
     static constexpr int kBytes = (4 * kWaveBytes > kRed) ? 4 * kWaveBytes : kRed;
     static_assert(kMaxWait < 64, "vmcnt holds 6 bits");
     static_assert(kSPR % 4 == 0, "scale rows of a super-step are whole dwords");
-    static_assert(!kHW || BITS % 2 == 0, "half slots: whole DMAs per half");
+    static_assert(BITS * kSW % 4 == 0, "part-super-step slots: whole DMAs per slot");
 };
 
 template <int BITS, int SB, int MT, int NT, int GS>
@@ -266,12 +273,12 @@ __device__ __forceinline__ void issue_x(const Ctx<BITS, SB, MT, NT, GS>& c, int 
 #pragma unroll
     for (int i = 0; i < L::kNX; i++) dma16(base + 1024u * i, src, c.xoff[i]);
 }
-// half-slot W (kHW): half hh (steps 2 hh, 2 hh + 1 of the part) into slot hh % 3
+// part-super-step W (kHW): unit g (steps kSW g .. kSW g + kSW - 1 of the part) into slot g % kRWW
 template <int BITS, int SB, int MT, int NT, int GS>
-__device__ __forceinline__ void issue_wh(const Ctx<BITS, SB, MT, NT, GS>& c, int hh) {
+__device__ __forceinline__ void issue_wh(const Ctx<BITS, SB, MT, NT, GS>& c, int g) {
     using L = Lay<BITS, SB, MT, NT, GS>;
-    const uint32_t slot = (uint32_t)(hh % 3);
-    const uint8_t* src = c.w + (size_t)hh * 16 * BITS;
+    const uint32_t slot = (uint32_t)(g % L::kRWW);
+    const uint8_t* src = c.w + (size_t)g * L::kWRow;
 #pragma unroll
     for (int ct = 0; ct < NT; ct++)
 #pragma unroll
@@ -307,6 +314,18 @@ __device__ __forceinline__ void issue_w(const Ctx<BITS, SB, MT, NT, GS>& c, int 
         }
 }
 
+// DMAs of the W and scale issues among steps q - kRX + 2 .. q (P = q % 4)
+template <class L, int NT, int P>
+constexpr int young_w() {
+    int n = 0;
+    for (int d = 0; d <= L::kRX - 2; d++) {
+        const int p = ((P - d) % 4 + 4) % 4;
+        if (p % L::kSW == 0) n += NT * L::kNWI;
+        if (p == 0) n += L::kNSS;
+    }
+    return n;
+}
+
 // step q (P = q % 4, compile time) of a wave whose part has nq steps
 template <int BITS, int TX, int SB, int MT, int NT, int GS, int P>
 __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, MT, NT, GS>& c, uint8_t* lw, int q,
@@ -318,11 +337,11 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     // fixed), once the previous step's reads of the refilled slots are done
     wait_lds_reads();
     if constexpr (L::kHW) {
-        // half 2 (u + P / 2) + 2 into the slot half - 1 used, at P == 0 also
-        // the scales of super-step u + 1
-        if constexpr (P == 0 || P == 2) {
-            const int hw = 2 * u + P / 2 + 2, hl = 2 * (nq >> 2) - 1;
-            issue_wh(c, hw < hl ? hw : hl);
+        // unit g + kLead into the slot unit g - 1 used, at the first step of
+        // unit g; at P == 0 also the scales of super-step u + 1
+        if constexpr (P % L::kSW == 0) {
+            const int gw = u * (4 / L::kSW) + P / L::kSW + L::kLead, gl = (nq >> 2) * (4 / L::kSW) - 1;
+            issue_wh(c, gw < gl ? gw : gl);
         }
         if constexpr (P == 0) {
             const int uw = u + 1, ul = (nq >> 2) - 1;
@@ -339,13 +358,10 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     // X(q) (and the older W(u)) landed: younger are the issues of steps
     // q - kRX + 2 .. q: kRX - 1 x issues, plus the W issue of the one of
     // those steps that starts a super-step, if any (P <= kRX - 2; kRX <= 5)
-    static_assert(L::kRX >= 2 && L::kRX <= (L::kHW ? 3 : 5), "one W issue at most among the younger steps");
-    // kHW: the W halves issued at the even steps among q - kRX + 2 .. q, the
-    // scales at the step among them that starts a super-step
-    constexpr int kYoung = (L::kRX - 1) * L::kNX +
-                           (L::kHW ? (P % 2 == 0 || L::kRX == 3 ? NT * L::kNWI : 0) +
-                                         (P <= L::kRX - 2 ? L::kNSS : 0)
-                                   : L::kNWS * (P <= L::kRX - 2 ? 1 : 0));
+    static_assert(L::kRX >= 2 && L::kRX <= 4, "W issued 4 steps ahead: older than the x awaited");
+    // the W issues of those steps: a slot's W at each step with P % kSW == 0,
+    // the scales (and, for whole slots, the W) at the one with P == 0
+    constexpr int kYoung = (L::kRX - 1) * L::kNX + young_w<L, NT, P>();
     wait_vmcnt_small<kYoung>();
     const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
     // x fragments
@@ -359,7 +375,7 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
     }
     // codes and scale of this lane's 32 codes in each column tile
     const int slot = u % L::kRW;
-    const int wslot = L::kHW ? (2 * u + P / 2) % 3 : slot;
+    const int wslot = L::kHW ? (u * (4 / L::kSW) + P / L::kSW) % L::kRWW : slot;
     const int wz = wswz<L::kWRow / 16>(j);
     const int gi = (P * 64 + 32 * h) / GS;
     uint32_t cw[NT][BITS];
@@ -370,7 +386,7 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
 #pragma unroll
         for (int i = 0; i < BITS; i++) {
             // within the row, before the swizzle (a half slot holds steps 2 (P / 2), + 1)
-            const int byte = (L::kHW ? P & 1 : P) * 8 * BITS + 4 * BITS * h + 4 * i;
+            const int byte = (P % L::kSW) * 8 * BITS + 4 * BITS * h + 4 * i;
             cw[ct][i] = *reinterpret_cast<const uint32_t*>(wrow + ((((byte >> 4) ^ wz) << 4) | (byte & 15)));
         }
         const uint8_t* sp = lw + L::kS0 + slot * L::kSS + ct * L::kST + j * L::kSPR + gi * L::kSb;
@@ -454,8 +470,8 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     // prologue: the issues of steps -kRX+1 .. -1 and super-steps up to kRW - 2
     // in the same order the steady state keeps (missing ones repeat step 0)
     if constexpr (L::kHW) {
-        issue_wh(c, 0);
-        issue_wh(c, 1);                    // a part has at least one super-step: two halves
+#pragma unroll
+        for (int g = 0; g < L::kLead; g++) issue_wh(c, g);  // a part has at least one super-step: 4 / kSW units
     }
 #pragma unroll
     for (int uu = 0; uu < L::kRW - 1; uu++) issue_w(c, uu < (nq >> 2) - 1 ? uu : (nq >> 2) - 1);

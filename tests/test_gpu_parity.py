@@ -453,12 +453,13 @@ def test_small_gemm_parity(ctx, oracle, bits, xd, sbd, od):
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, F32, F32)])
 def test_small_gemm_two_tiles_parity(ctx, oracle, bits, xd, sbd, od):
     """Past 256 column tiles of 32 (N > 8192) the small-M GEMM runs two tiles
-    per block where their rings fit (6- and 8-bit codes through half-super-
-    step W slots; 8-bit blocks with two M tiles, and 6/8-bit ones with f32
-    scales at group 32, keep one tile and run two rounds): ragged N with the
-    last block's second tile wholly past N (N = 8200), group sizes 32 (the
-    rings fill the 160 KB exactly for 4-bit codes with f32 scales and 8-bit
-    ones with 16-bit scales), 64 and 128, one and two M tiles."""
+    per block where their rings fit (6- and 8-bit codes through half- or
+    quarter-super-step W slots; blocks with f32 scales at group 32 and 8-bit
+    codes, or 6-bit ones at two M tiles, keep one tile and run two rounds):
+    ragged N with the last block's second tile wholly past N (N = 8200),
+    group sizes 32 (the rings fill the 160 KB exactly for 4-bit codes with
+    f32 scales and 8-bit ones with 16-bit scales), 64 and 128, one and two M
+    tiles."""
     O = oracle
     for (M, K, N, gs) in [(64, 1024, 8200, 32), (17, 2048, 9000, 64), (40, 1024, 12345, 128),
                           (32, 1024, 8400, 32)]:
@@ -517,6 +518,7 @@ def test_split_k_shapes_in_sequence(ctx, oracle):
     (32, 8192, 8192, 8, 128, BF16, "gemm"),   # small-M GEMM, one block per CU
     (64, 4096, 11008, 3, 64, F16, "gemm"),    # two M tiles, two column tiles per block, ragged grid
     (64, 4096, 11008, 6, 64, F16, "gemm"),    # the same with the 6-bit half-slot W ring
+    (64, 4096, 11008, 8, 64, F16, "gemm"),    # the same with the 8-bit quarter-slot W ring
     (32, 8192, 16384, 4, 64, BF16, "gemm"),   # one M tile, two column tiles per block, 256 blocks
     (32, 4096, 14336, 8, 128, BF16, "gemm"),  # the same with the 8-bit half-slot W ring
     (16, 4096, 14336, 4, 64, BF16, "gemv"),   # mid-M GEMV rings
