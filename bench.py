@@ -103,14 +103,52 @@ class Hip:
         self.ck(self.L.hipFree(p), "hipFree")
 
 
-def time_launches(hip, stream, step, steps, warmup):
-    """`warmup` untimed launches, then exactly `steps` launches back to back
-    on `stream` between a synchronize on each side; returns host wall time of
-    the region and the HIP-event time per launch.  step(i) enqueues launch i
-    (rotating over the weight copies itself)."""
-    for i in range(warmup):
-        step(i)
+# Every leg first runs its own launches for at least this long (and at least
+# --warmup launches): a leg that follows seconds of host-side set-up (weight
+# generation, upload) otherwise starts on a GPU whose clocks are still
+# ramping, which a handful of warm-up launches does not cover.
+WARM_S = 0.3
+
+
+def warm(hip, stream, step, launches, warm_s=WARM_S):
+    """At least `launches` launches and at least warm_s seconds of them
+    (batches of launches, a synchronize after each, until both hold)."""
+    t0, n = time.perf_counter(), 0
+    while True:
+        for _ in range(max(1, min(launches, 64))):
+            step(n)
+            n += 1
+        hip.sync(stream)
+        if n >= launches and time.perf_counter() - t0 >= warm_s:
+            return n
+
+
+def per_launch_us(hip, stream, step, steps):
+    """The same launches again with an event before each and one after the
+    last: the median and spread of the per-launch durations (kernel plus the
+    gap to the next launch), and the first three (a clock ramp shows there)."""
+    ev = [hip.event() for _ in range(steps + 1)]
     hip.sync(stream)
+    for i in range(steps):
+        hip.record(ev[i], stream)
+        step(i)
+    hip.record(ev[steps], stream)
+    hip.sync(stream)
+    d = np.array([hip.elapsed_ms(ev[i], ev[i + 1]) * 1e3 for i in range(steps)])
+    for e in ev:
+        hip.L.hipEventDestroy(e)
+    return {"median": round(float(np.median(d)), 3), "p10": round(float(np.percentile(d, 10)), 3),
+            "p90": round(float(np.percentile(d, 90)), 3), "first": [round(float(v), 3) for v in d[:3]]}
+
+
+def time_launches(hip, stream, step, steps, warmup):
+    """Warm-up (warm(): at least `warmup` launches and WARM_S seconds), then
+    exactly `steps` launches back to back on `stream` between a synchronize
+    on each side; returns host wall time of the region and the HIP-event
+    time per launch, then the per-launch durations of the same launches run
+    once more (per_launch_us).  step(i) enqueues launch i (rotating over the
+    weight copies itself)."""
+    warm(hip, stream, step, warmup)
     e0, e1 = hip.event(), hip.event()
     hip.sync(stream)
     t0 = time.perf_counter()
@@ -120,7 +158,9 @@ def time_launches(hip, stream, step, steps, warmup):
     hip.record(e1, stream)
     hip.sync(stream)
     wall = time.perf_counter() - t0
-    return {"wall_s": wall, "event_ms_per_launch": hip.elapsed_ms(e0, e1) / steps}
+    r = {"wall_s": wall, "event_ms_per_launch": hip.elapsed_ms(e0, e1) / steps}
+    r["per_launch_us"] = per_launch_us(hip, stream, step, steps)
+    return r
 
 
 def time_graph(hip, stream, step, reps=32):
@@ -289,15 +329,17 @@ def host_info():
             "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
 
 
-def _timed(fn, budget_s, min_calls=3):
-    fn()
-    n, t0 = 0, time.perf_counter()
-    while True:
+def _timed(fn, budget_s, min_calls=10, warmups=3):
+    """`warmups` untimed calls, then timed calls until there are at least
+    min_calls and budget_s seconds of them; the per-call seconds."""
+    for _ in range(warmups):
         fn()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s and n >= min_calls:
-            return n, el
+    ts, t_start = [], time.perf_counter()
+    while len(ts) < min_calls or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return ts
 
 
 def ref_cpu_backend():
@@ -327,13 +369,16 @@ def cpu_baseline(M, K, N, bits, gs, budget_s=4.0):
     def port(t):
         return lambda: O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F16, F16, F16, variant="omp", threads=t)
 
-    n_all, el_all = _timed(port(threads), budget_s)
-    n_one, el_one = _timed(port(1), budget_s)
-    out = {"value": round(wb * n_all / el_all / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-           "sample": f"{n_all} calls of the OpenMP CPU quantized GEMV (oracle), M={M} K={K} N={N} "
-                     f"{bits}-bit g{gs} f16, {el_all:.1f} s on {threads} threads",
-           "one_core": {"value": round(wb * n_one / el_one / 1e9, 3), "unit": "GB/s", "cores": 1,
-                        "sample": f"{n_one} calls, {el_one:.1f} s"},
+    t_all = _timed(port(threads), budget_s)
+    t_one = _timed(port(1), budget_s)
+    med_all, med_one = float(np.median(t_all)), float(np.median(t_one))
+    out = {"value": round(wb / med_all / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"median of {len(t_all)} timed calls (after 3 warm-up calls) of the OpenMP CPU "
+                     f"quantized GEMV (oracle), M={M} K={K} N={N} {bits}-bit g{gs} f16, "
+                     f"{sum(t_all):.1f} s on {threads} threads",
+           "mean_value": round(wb * len(t_all) / sum(t_all) / 1e9, 3),
+           "one_core": {"value": round(wb / med_one / 1e9, 3), "unit": "GB/s", "cores": 1,
+                        "sample": f"median of {len(t_one)} calls after 3 warm-ups, {sum(t_one):.1f} s"},
            "host": info}
     ref = ref_cpu_backend()
     if ref is None:
@@ -354,15 +399,15 @@ def cpu_baseline(M, K, N, bits, gs, budget_s=4.0):
             if vt.op_matmul_f32(ctx, bx, bw, by, M, K, N) != 0:
                 raise RuntimeError("reference op_matmul_f32")
 
-        n_ref, el_ref = _timed(compose, budget_s, min_calls=2)
+        t_ref = _timed(compose, 0.0)
         for h in (bx, bw, by):
             vt.buffer_free(ctx, h)
         vt.destroy_context(ctx)
         out["reference_composition"] = {
-            "value": round(wb * n_ref / el_ref / 1e9, 3), "unit": "GB/s", "kind": "reference",
+            "value": round(wb / float(np.median(t_ref)) / 1e9, 3), "unit": "GB/s", "kind": "reference",
             "cores": int(os.environ.get("OMP_NUM_THREADS", "0")) or info["nproc"],
-            "sample": f"{n_ref} calls of host dequantize to f32 W^T + reference cpu_op_matmul_f32 "
-                      f"(src/cpu_backend.cpp:243-266, OpenMP), {el_ref:.1f} s"}
+            "sample": f"median of {len(t_ref)} calls (after 3 warm-ups) of host dequantize to f32 W^T + "
+                      f"reference cpu_op_matmul_f32 (src/cpu_backend.cpp:243-266, OpenMP), {sum(t_ref):.1f} s"}
     return out
 
 
@@ -418,6 +463,45 @@ def parse_shape(spec):
     return ("shape", int(f[0]), int(f[1]), int(f[2]), int(f[3]), int(f[4]), dt, dt, dt)
 
 
+def copies_for(wb):
+    """Rotated weight copies: together at least 2.2 x the 256 MB Infinity
+    Cache, so each launch streams its weights from HBM (4..64 copies)."""
+    return max(4, min(64, -(-int(2.2 * (256 << 20)) // wb)))
+
+
+# the BASELINE configs the headline line does not already time (configs[0],
+# [2] and [4]; [1] and [3] are the headline, decode and GEMM legs)
+CONFIG_LEGS = [s for s in SWEEP if s[0] in ("c0", "c2", "c4")]
+
+
+def config_legs(ctx, hip, steps, warmup, keep=False):
+    """One entry per CONFIG_LEGS shape, timed as the headline is: the kernel
+    class AUTO picks, mean and median us per launch, graph replays, and the
+    weight-byte and flop rates with their roofline fractions.  keep=True
+    also returns the c2 run (inputs and output) for the parity check."""
+    from mlx_amd import abi
+    names = {abi.KERNEL_GEMV: "gemv", abi.KERNEL_GEMM: "gemm"}
+    out, runs = {}, {}
+    for name, M, K, N, bits, gs, xd, sbd, od in CONFIG_LEGS:
+        wb = weight_bytes(N, K, bits, gs, sbd)
+        r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, abi.KERNEL_AUTO,
+                      copies=copies_for(wb), keep=keep and name == "c2")
+        t = r["event_ms_per_launch"] * 1e-3
+        flops = 2.0 * M * N * K
+        key = f"{name}_m{M}_{bits}bit"
+        out[key] = {"M": M, "K": K, "N": N, "bits": bits, "group_size": gs,
+                    "kernel": names.get(ctx.select_kernel(M, K, N, gs, bits, xd, sbd), "?"),
+                    "kernel_us_avg": round(t * 1e6, 3), "kernel_us_median": r["per_launch_us"]["median"],
+                    "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
+                    "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
+                    "tflops": round(flops / t / 1e12, 2),
+                    "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4),
+                    "copies": copies_for(wb)}
+        if keep and name == "c2":
+            runs["c2"] = r
+    return out, runs
+
+
 def sweep(ctx, hip, steps, only=None, table=SWEEP):
     """One line per config: kernel AUTO picks, per-launch time (stream and
     graph replays), weight GB/s and TFLOP/s with their roofline fractions."""
@@ -427,13 +511,14 @@ def sweep(ctx, hip, steps, only=None, table=SWEEP):
         if only and name not in only:
             continue
         kern = ctx.select_kernel(M, K, N, gs, bits, xd, sbd)
-        copies = 4 if M >= 256 else COPIES
+        copies = 4 if M >= 256 else copies_for(weight_bytes(N, K, bits, gs, sbd))
         r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, 8, abi.KERNEL_AUTO, copies=copies)
         t = r["event_ms_per_launch"] * 1e-3
         wb = weight_bytes(N, K, bits, gs, sbd)
         flops = 2.0 * M * N * K
         print(json.dumps({"config": name, "M": M, "K": K, "N": N, "bits": bits, "group_size": gs,
                           "kernel": names.get(kern, str(kern)), "us": round(t * 1e6, 3),
+                          "us_median": r["per_launch_us"]["median"],
                           "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                           "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
                           "tflops": round(flops / t / 1e12, 2),
@@ -448,7 +533,8 @@ def decode_legs(ctx, hip, K, N, bits, gs, steps, warmup):
     for m in (4, 8):
         r = bench_qmm(ctx, hip, m, K, N, bits, gs, F16, F16, F16, steps, warmup, abi.KERNEL_AUTO)
         t = r["event_ms_per_launch"] * 1e-3
-        out[f"M{m}"] = {"kernel_us_avg": round(t * 1e6, 3), "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
+        out[f"M{m}"] = {"kernel_us_avg": round(t * 1e6, 3), "kernel_us_median": r["per_launch_us"]["median"],
+                        "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                         "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4)}
     return out
 
@@ -529,12 +615,14 @@ def main():
             if ctx.select_kernel(2048, 4096, n, 64, 4, BF16) != abi.KERNEL_GEMM:
                 break
             steps = min(args.steps, 256)
-            rg = bench_qmm(ctx, hip, 2048, 4096, n, 4, 64, BF16, BF16, BF16, steps, 8, abi.KERNEL_AUTO,
-                           copies=4, keep=keep and n == 4096)
+            rg = bench_qmm(ctx, hip, 2048, 4096, n, 4, 64, BF16, BF16, BF16, steps, args.warmup,
+                           abi.KERNEL_AUTO, copies=4, keep=keep and n == 4096)
             flops = 2.0 * 2048 * 4096 * n
             tf = flops / (rg["event_ms_per_launch"] * 1e-3) / 1e12
             gemm[f"N{n}"] = {"tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                              "kernel_us_avg": round(rg["event_ms_per_launch"] * 1e3, 2),
+                             "kernel_us_median": rg["per_launch_us"]["median"],
+                             "per_launch_us": rg["per_launch_us"],
                              "graph_us": round(rg["graph_ms_per_launch"] * 1e3, 2),
                              "wall_tflops": round(flops * rg["steps"] / rg["wall_s"] / 1e12, 2)}
             runs[n] = rg
@@ -570,6 +658,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(GEMV_PROFILE),
                      "kernel": "qgemv_line_kernel", "kernel_us_avg": round(t * 1e6, 3),
+                     "kernel_us_median": r["per_launch_us"]["median"], "per_launch_us": r["per_launch_us"],
                      "graph_us_per_launch": round(r["graph_ms_per_launch"] * 1e3, 3),
                      "graph_frac": round(wb / r["graph_ms_per_launch"] / 1e6 / HBM_PEAK_GBS, 4),
                      "algorithmic_bytes": wb, "timing": "HIP events around the timed launches on the plugin stream"},
@@ -580,13 +669,12 @@ def main():
     gemm_runs = {}
     if not args.no_gemm:
         line["gemm_m2048"], gemm_runs = gemm_legs(keep)
-    c2 = None
+    line["configs"], cfg_runs = config_legs(ctx, hip, min(args.steps, 256), args.warmup, keep)
     # c2's kernel family decides its semantics (the GEMM kernels dequantize
     # to the activation type before the multiply)
     c2_gemm = ctx.select_kernel(32, 8192, 8192, 128, 8, BF16) == abi.KERNEL_GEMM
     if keep:
-        c2 = bench_qmm(ctx, hip, 32, 8192, 8192, 8, 128, BF16, BF16, BF16, 64, 8, abi.KERNEL_AUTO,
-                       copies=4, keep=True)
+        c2 = cfg_runs["c2"]
         c2f = bench_qmm(ctx, hip, 32, 8192, 8192, 8, 128, BF16, BF16, F32, 16, 4, abi.KERNEL_AUTO,
                         copies=4, keep=True)
     ctx.close()

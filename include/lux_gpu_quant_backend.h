@@ -198,8 +198,13 @@ __attribute__((visibility("default"))) bool lux_gpu_backend_quant_init(const lux
  * device memory (code under HIP graph capture, serving loops that forbid
  * hipMalloc).  x, w_q, scales, biases and out are device pointers of the
  * current device holding at least the bytes the shape needs (not checked:
- * there are no buffer sizes here); `stream` is a hipStream_t of that device
- * (NULL: the null stream).  Same kernels, selection, results and shape and
+ * there are no buffer sizes here), and each of x, w_q, scales and biases
+ * must be followed by at least 256 readable bytes of device memory (not
+ * used for the result: the kernels copy operand arrays in whole 16-byte
+ * chunks and may read up to 255 bytes past an array's end; the plugin's own
+ * buffers carry that slack, so an operand carved from the end of a larger
+ * allocation needs 256 bytes left after it).  `stream` is a hipStream_t of
+ * that device (NULL: the null stream).  Same kernels, selection, results and shape and
  * dtype errors as op_quantized_matmul_ex.  The partial sums, tile counters
  * and flags of the split-K small-M GEMM and of the large GEMM's split last
  * round live in a 16 MiB (+ 4 KiB) static device array that
@@ -207,7 +212,10 @@ __attribute__((visibility("default"))) bool lux_gpu_backend_quant_init(const lux
  * are INVALID_ARGUMENT; the split rule keeps every shape within it).  All
  * calls on one GPU share that array: calls that overlap in time on one GPU
  * (concurrent streams, or threads) race and give wrong results.  The first
- * call on a device clears the array with a kernel on its stream.
+ * call on a device clears the array with a kernel on its stream, so that
+ * call must not be made under stream capture: it returns NOT_SUPPORTED
+ * there (make one eager call on the device first; later calls may be
+ * captured and replayed).
  */
 __attribute__((visibility("default"))) LuxBackendError lux_gpu_quantized_matmul_noalloc(
     const void* x, const void* w_q, const void* scales, const void* biases, void* out, int M, int K, int N,

@@ -33,11 +33,21 @@ __global__ void clear_words(uint32_t* p, size_t n) {
 
 // once per device, with that device current: look up the array's device
 // address and clear it (a kernel on `st`, ordered before this call's work;
-// the GEMMs return their counters and flags to zero after every launch)
+// the GEMMs return their counters and flags to zero after every launch).
+// That first call must not be under stream capture: the clear would become
+// a node of the caller's graph and run on every replay, after later calls
+// have relied on the array being clear once.  It is refused instead.
 LuxBackendError scratch_on(int dev, hipStream_t st, void** out) {
     std::lock_guard<std::mutex> lock(g_mu);
     if (g_scratch[dev] == nullptr) {
         if (!lux_hip_is_gfx950(dev)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
+        // (a stream the query rejects is left to the launch below to report)
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+            (void)hipGetLastError();
+            cap = hipStreamCaptureStatusNone;
+        }
+        if (cap != hipStreamCaptureStatusNone) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
             (void)hipGetLastError();

@@ -97,11 +97,93 @@ def test_noalloc_matches_context_op(ctx, oracle):
         hip.ck(hip.L.hipStreamDestroy(stream), "hipStreamDestroy")
 
 
-def test_noalloc_errors():
-    """Errors come back before any device work: null pointers, a bad shape."""
+def test_noalloc_back_to_back(ctx, oracle):
+    """The split-K and split-last-round calls of CALLS enqueued on one stream
+    with no synchronize between them (the scratch's counters and flags must
+    be back at zero when the next call starts), then each output against the
+    context op on the same inputs, bit for bit."""
+    from mlx_amd import runtime
+    O = oracle
     f = _entry()
-    p = ctypes.c_void_p(16)
-    assert f(None, p, p, p, p, 16, 256, 8, 64, 4, F16, F16, F16, 0, None) == 1  # INVALID_ARGUMENT
-    assert f(p, p, p, p, p, 16, 100, 8, 64, 4, F16, F16, F16, 0, None) == 1     # K % group size
-    assert f(p, p, p, p, p, 16, 256, 8, 64, 7, F16, F16, F16, 0, None) != 0     # bits outside the format
-    assert f(p, p, p, p, p, 16, 256, 8, 64, 4, F16, F16, F16, 9, None) == 1     # unknown kernel
+    hip = _Hip()
+    stream = ctypes.c_void_p()
+    hip.ck(hip.L.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    calls, held = CALLS[:4] * 2, []
+    try:
+        for i, (M, K, N, bits, gs, xd, sbd, od, kern) in enumerate(calls):
+            print(f"[case] noalloc back-to-back call {i}: M={M} K={K} N={N} b={bits} kernel={kern}", flush=True)
+            x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=700 + i % 4)
+            ptrs = [hip.upload(np.ascontiguousarray(a)) for a in (x, w_q, s, b)]
+            out = hip.alloc(M * N * runtime.esize(od))
+            held.append((ptrs, out, (x, w_q, s, b), (M, K, N, bits, gs, xd, sbd, od, kern)))
+            rc = f(*ptrs, out, M, K, N, gs, bits, xd, sbd, od, kern, stream)
+            assert rc == 0, f"noalloc returned {rc}"
+        hip.ck(hip.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
+        for i, (ptrs, out, host, (M, K, N, bits, gs, xd, sbd, od, kern)) in enumerate(held):
+            got = hip.download(out, runtime.np_dtype(od), (M, N))
+            want = runtime.run_quantized_matmul(ctx, *host, M, K, N, gs, bits, xd, sbd, od, kern)
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"call {i} differs from the context op"
+    finally:
+        for ptrs, out, _, _ in held:
+            for p in ptrs + [out]:
+                hip.free(p)
+        hip.ck(hip.L.hipStreamDestroy(stream), "hipStreamDestroy")
+
+
+def test_noalloc_graph_capture(ctx, oracle):
+    """One split-K call (parts meeting in the scratch) captured into a HIP
+    graph after an eager call on the device, the graph replayed three times
+    with the host's own synchronizations and downloads between replays;
+    every replay equals the context op bit for bit."""
+    from mlx_amd import runtime
+    O = oracle
+    f = _entry()
+    hip = _Hip()
+    M, K, N, bits, gs, xd, sbd, od, kern = CALLS[0]
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=760)
+    want = runtime.run_quantized_matmul(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, kern)
+    stream = ctypes.c_void_p()
+    hip.ck(hip.L.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    ptrs = [hip.upload(np.ascontiguousarray(a)) for a in (x, w_q, s, b)]
+    out = hip.alloc(M * N * runtime.esize(od))
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    try:
+        # the eager call sets the scratch up on this device (a first call may not be captured)
+        assert f(*ptrs, out, M, K, N, gs, bits, xd, sbd, od, kern, stream) == 0
+        hip.ck(hip.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
+        hip.ck(hip.L.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")  # global mode
+        rc = f(*ptrs, out, M, K, N, gs, bits, xd, sbd, od, kern, stream)
+        hip.ck(hip.L.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        assert rc == 0, f"captured noalloc call returned {rc}"
+        hip.ck(hip.L.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+        for rep in range(3):
+            print(f"[case] noalloc graph replay {rep}", flush=True)
+            hip.ck(hip.L.hipMemset(out, 0xFF, ctypes.c_size_t(M * N * runtime.esize(od))), "hipMemset")
+            hip.ck(hip.L.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+            hip.ck(hip.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
+            got = hip.download(out, runtime.np_dtype(od), (M, N))
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), f"replay {rep} differs"
+    finally:
+        if exe.value:
+            hip.L.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.L.hipGraphDestroy(graph)
+        for p in ptrs + [out]:
+            hip.free(p)
+        hip.ck(hip.L.hipStreamDestroy(stream), "hipStreamDestroy")
+
+
+def test_noalloc_errors():
+    """Errors come back before any device work: null pointers, a bad shape.
+    The pointers are real (small) device allocations, so a check that ran
+    after a launch would still not touch unmapped memory."""
+    f = _entry()
+    hip = _Hip()
+    p = hip.alloc(4096)
+    try:
+        assert f(None, p, p, p, p, 16, 256, 8, 64, 4, F16, F16, F16, 0, None) == 1  # INVALID_ARGUMENT
+        assert f(p, p, p, p, p, 16, 100, 8, 64, 4, F16, F16, F16, 0, None) == 1     # K % group size
+        assert f(p, p, p, p, p, 16, 256, 8, 64, 7, F16, F16, F16, 0, None) != 0     # bits outside the format
+        assert f(p, p, p, p, p, 16, 256, 8, 64, 4, F16, F16, F16, 9, None) == 1     # unknown kernel
+    finally:
+        hip.free(p)
