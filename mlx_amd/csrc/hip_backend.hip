@@ -40,6 +40,9 @@ struct HipContext {
     // allocates; used only by work on `stream`, which orders its users
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // launches on ws so far: each GEMM launch gets the next number as its
+    // epoch (the split tiles meet by it; never 0)
+    uint32_t epoch = 0;
 };
 
 
@@ -298,7 +301,8 @@ int gemv_max_m(int K, int bits, LuxBackendDtype x_dtype) {
 //    x, W and f32 scales below 2 GiB; or
 //  * K a multiple of 256 (the large kernel's scale windows span 4 K steps of
 //    64), x and W below 4 GiB (32-bit offsets), and its LDS buffers within
-//    one CU's 160 KB (f32 scales at group size 32 with 6- or 8-bit codes do
+//    one CU's 160 KB (f32 scales at group size 32 with 6-bit codes, and with
+//    8-bit codes where K % 1024 != 0, do
 //    not fit)
 bool gemm_ok(int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dtype,
              LuxBackendDtype sb_dtype) {
@@ -306,7 +310,9 @@ bool gemm_ok(int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dt
     if (M > 8 && M <= 64 && K % 128 == 0 && (size_t)M * K * 2 < (1ull << 31) &&
         (size_t)N * K * bits / 8 < (1ull << 31) && (size_t)N * (K / 32) * 4 < (1ull << 31))
         return true;
-    if (sb_dtype == LUX_DTYPE_FLOAT32 && group_size == 32 && bits >= 6) return false;
+    // (the register-W kernel, 4/8-bit codes with K % 1024 == 0, fits them all)
+    if (sb_dtype == LUX_DTYPE_FLOAT32 && group_size == 32 && bits >= 6 && !(bits == 8 && K % 1024 == 0))
+        return false;
     return K % 256 == 0 && (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
 }
 
@@ -389,6 +395,8 @@ LuxBackendError qmm_impl(LuxBackendContext* c, LuxBackendBuffer* x, LuxBackendBu
     a.act = act;
     a.ws = ctx->ws;
     a.ws_bytes = ctx->ws_bytes;
+    if (++ctx->epoch == 0u) ctx->epoch = 1u;
+    a.epoch = ctx->epoch;
 
     if (hipSetDevice(ctx->device) != hipSuccess) return LUX_BACKEND_ERROR_DEVICE_LOST;
     return lux_hip_qmm_dispatch(a, kernel, ctx->stream);

@@ -42,6 +42,10 @@ struct QmmArgs {
     // (counters zero between launches); null/0: kernels that need one are skipped
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // launch number on this workspace: never zero, never repeated for one
+    // workspace (the large GEMMs' split tiles meet by it, qsplit.h); 0: no
+    // split tiles
+    uint32_t epoch = 0;
     Epilogue epi() const { return Epilogue{bias, bias_dtype, act, out_dtype}; }
     // kernels are instantiated with and without the output stage: the plain
     // op runs code with no bias or activation path at all
@@ -79,6 +83,9 @@ size_t qgemm_sk_workspace(int M, int K, int N, int bits, int x_dtype, size_t cap
 // and the large GEMM's split last round (at most 128 tiles, one K half of
 // 128 KiB each).  The first KiB holds tile counters and flags.
 constexpr size_t kSplitWorkspaceBytes = (16u << 20) + 4096;
+// MFMA GEMM for large M with each wave's W operand dequantized in its own
+// registers: 4/8-bit codes, f16/bf16 x, K % 1024 == 0; NotSupported otherwise
+LuxStatus launch_qgemm_rw(const QmmArgs& a, hipStream_t st);
 // MFMA GEMM for f16/bf16 activations; needs K % 64 == 0
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st);
 // generic one-thread-per-output kernel for shapes the tiled kernels reject

@@ -1,5 +1,7 @@
 // qgemm.hip -- dispatch of the MFMA dequant GEMM (kernels in qgemm_impl.h,
 // one translation unit per group size: qgemm_g{32,64,128}.hip).
+#include <cstdlib>
+
 #include "qgemm_impl.h"
 
 namespace lxq {
@@ -10,6 +12,16 @@ LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st) {
         LuxStatus s = launch_qgemm_sk(a, st);
         if (s != LuxStatus::NotSupported) return s;
         s = launch_qgemm_small(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
+    // 4/8-bit codes with K % 1024 == 0: the register-W kernel (unless
+    // LUX_HIP_GEMM_RW=0 asks for the LDS-dequant kernel below)
+    static const bool rw_on = [] {
+        const char* e = std::getenv("LUX_HIP_GEMM_RW");
+        return !(e && e[0] == '0');
+    }();
+    if (rw_on) {
+        const LuxStatus s = launch_qgemm_rw(a, st);
         if (s != LuxStatus::NotSupported) return s;
     }
     // the scale windows cover 4 K steps of 64 codes

@@ -45,6 +45,7 @@
 #pragma once
 #include "kernels.h"
 #include "qcommon.h"
+#include "qsplit.h"
 
 namespace lxq {
 namespace gemm {
@@ -62,17 +63,12 @@ constexpr int kThreads = 512;  // 8 waves: two per SIMD
 constexpr int kXStageBytes = BM * BK * 2;  // 32768
 constexpr int kXStages = 3;
 constexpr int kWStageBytes = BN * BK * 2;  // 16384
-// tail split: CUs of the target (MI355X: 256), the workspace layout (tile
-// counters in its first KiB, shared with the split-K small-M GEMM, which
-// never runs at the same time on a context; partial tiles from 4 KiB on)
+// tail split: CUs of the target (MI355X: 256); the workspace layout and the
+// protocol of the split tiles are qsplit.h's
 constexpr int kCUs = 256;
 constexpr uint32_t kSplitSlotBytes = BM * BN * 4;  // one K half of one tile, fp32
-constexpr size_t kSplitPartOffset = 4096;
-constexpr int kSplitFlagWord = 128;                 // flags after the 128 counters
-constexpr int kCachePolicyDevice = 16;             // buffer cache policy sc1
-static_assert(kSplitPartOffset + (size_t)kCUs / 2 * kSplitSlotBytes <= kSplitWorkspaceBytes, "workspace size");
-static_assert(kCUs / 2 <= kSplitFlagWord && (kSplitFlagWord + kCUs / 2) * 4 <= 1024,
-              "split-tile counters and flags within the first KiB");
+static_assert(split::kPartOffset + (size_t)kCUs / 2 * kSplitSlotBytes <= kSplitWorkspaceBytes, "workspace size");
+static_assert(kCUs / 2 <= split::kMaxHalfTiles, "split tiles within the workspace's counter words");
 
 // chunk position permutation of LDS row r (bijective on the 8 chunks; rows
 // r and r + 8 get different permutations)
@@ -514,7 +510,7 @@ template <int TX, int BITS, int SB, int GS, bool EPI>
 __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep,
-    int mtiles, int split_from, void* __restrict__ ws) {
+    int mtiles, int split_from, void* __restrict__ ws, uint32_t epoch) {
     static_assert(lds_fits<BITS, GS, SB>(), "LDS budget");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -576,32 +572,24 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
         main_loop<TX, BITS, SB, GS, 1>(acc, t, scales, biases);
 
     if (part >= 0) {
-        // A K half of a split tile.  The two halves count in on the tile's
-        // counter; the first stores its fp32 sums into slot (split tile) of
-        // the workspace -- vector q of thread tid at byte ((slot * 16 + q) *
-        // 512 + tid) * 16 -- and then raises the tile's flag; the second
-        // waits for the flag, adds those sums to its own and stores y.  The
-        // wait is for a block that has already counted in, so it is resident
-        // and past its K loop, with nothing left to wait for itself.  The
-        // sums, counters and flags are written and read with the
-        // device-scope cache policy (sc1): the halves may run on different
-        // XCDs, whose L2s are not coherent with each other.
+        // A K half of a split tile: the halves meet in the workspace by the
+        // protocol of qsplit.h.  The first to arrive stores its fp32 sums --
+        // vector q of thread tid at byte ((slot * 16 + q) * 512 + tid) * 16
+        // -- and publishes; the second waits, adds them to its own and
+        // stores y.  The count's outcome goes through the first LDS word:
+        // every wave's transfers have landed (the K loop ends waiting for
+        // them all), so nothing writes the x stages any more (a static LDS
+        // variable would push the buffers that fill the 160 KB exactly past
+        // the limit).
         const int st = tile - split_from;
-        uint32_t* counters = static_cast<uint32_t*>(ws);
-        uint32_t* flags = counters + kSplitFlagWord;
-        const __amdgpu_buffer_rsrc_t pr = make_rsrc(static_cast<uint8_t*>(ws) + kSplitPartOffset,
+        const __amdgpu_buffer_rsrc_t pr = make_rsrc(static_cast<uint8_t*>(ws) + split::kPartOffset,
                                                     (uint32_t)((gridDim.x - (unsigned)split_from) >> 1) * kSplitSlotBytes);
         const uint32_t voff = (uint32_t)tid * 16u;
-        // the count's outcome goes through the first LDS word: every wave's
-        // transfers have landed (the K loop ends waiting for them all), so
-        // nothing writes the x stages any more (a static LDS variable would
-        // push the buffers that fill the 160 KB exactly past the limit)
         uint32_t* word = reinterpret_cast<uint32_t*>(lds);
         __syncthreads();
-        if (tid == 0)
-            *word = __hip_atomic_fetch_add(&counters[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) *word = split::arrive_first(ws, st) ? 1u : 0u;
         __syncthreads();
-        if (*word == 0u) {
+        if (*word == 1u) {
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 const f32x16& a = acc[q >> 3][(q >> 2) & 1];
@@ -609,32 +597,23 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(
                 __builtin_amdgcn_raw_buffer_store_b128(
                     v4{__float_as_uint(a[v]), __float_as_uint(a[v + 1]), __float_as_uint(a[v + 2]),
                        __float_as_uint(a[v + 3])},
-                    pr, voff, (uint32_t)(st * 16 + q) * (kThreads * 16u), kCachePolicyDevice);
+                    pr, voff, (uint32_t)(st * 16 + q) * (kThreads * 16u), split::kCachePolicyDevice);
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            if (tid == 0) __hip_atomic_store(&flags[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) split::publish(ws, st, epoch);
             return;
         }
-        // the second half: wait for the first's sums (bounded: a flag never
-        // raised within ~2^22 polls marks the tile NaN instead of hanging),
-        // then set the counter and the flag back to zero for the next launch
-        if (tid == 0) {
-            uint32_t polls = 0;
-            while (__hip_atomic_load(&flags[st], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
-                   ++polls < (1u << 22))
-                __builtin_amdgcn_s_sleep(2);
-            *word = polls < (1u << 22) ? 1u : 2u;
-            __hip_atomic_store(&flags[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&counters[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        // the second half: the first's sums, or NaN for a tile whose partner
+        // never published (bounded wait)
+        if (tid == 0) *word = split::wait_partner(ws, st, epoch) ? 2u : 3u;
         __syncthreads();
-        const float fail = *word == 1u ? 0.f : __builtin_nanf("");
+        const float fail = *word == 2u ? 0.f : __builtin_nanf("");
         v4 o[16];
 #pragma unroll
         for (int q = 0; q < 16; q++)
             o[q] = __builtin_amdgcn_raw_buffer_load_b128(pr, voff, (uint32_t)(st * 16 + q) * (kThreads * 16u),
-                                                         kCachePolicyDevice);
+                                                         split::kCachePolicyDevice);
 #pragma unroll
         for (int q = 0; q < 16; q++) {
             f32x16& a = acc[q >> 3][(q >> 2) & 1];
@@ -699,13 +678,13 @@ LuxStatus launch4_e(const QmmArgs& a, hipStream_t st) {
         // half full (each half a whole number of 4-step scale windows)
         const int r = tiles % kCUs;
         const int split_from =
-            r > 0 && 2 * r <= kCUs && (a.K / BK) % 8 == 0 && a.ws != nullptr &&
-                    a.ws_bytes >= kSplitPartOffset + (size_t)r * kSplitSlotBytes
+            r > 0 && 2 * r <= kCUs && (a.K / BK) % 8 == 0 && a.ws != nullptr && a.epoch != 0u &&
+                    a.ws_bytes >= split::kPartOffset + (size_t)r * kSplitSlotBytes
                 ? tiles - r
                 : tiles;
         hipLaunchKernelGGL(kern, dim3(tiles + (tiles - split_from)), dim3(kThreads), lds, st,
                            static_cast<const uint16_t*>(a.x), a.wq, a.scales, a.biases, a.y, a.M, a.K,
-                           a.N, a.epi(), mtiles, split_from, a.ws);
+                           a.N, a.epi(), mtiles, split_from, a.ws, a.epoch);
         return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
     }
 }

@@ -34,6 +34,7 @@
 #include <type_traits>
 
 #include "qgemm_small.h"
+#include "qsplit.h"
 
 namespace lxq {
 namespace sk {
@@ -50,7 +51,7 @@ constexpr int kCols = 128;   // output columns (W rows) per block
 constexpr int kSS = 128;     // codes of K per super-step
 constexpr int PD = 4;        // super-steps of loads in flight (<= 168 VGPRs: 2 waves per SIMD)
 
-// workspace: [tile counters: kCounterBytes][partials: tiles x S parts x M
+// workspace: [tile counters: kCounterBytes]..[partials from kPartBase: tiles x S parts x M
 // tiles x 16 KiB].  The counter region has one fixed size for every launch:
 // K is split only when there are fewer than 256 tiles, and a counter slot
 // must never be written by another shape's partials (its count would then
@@ -59,8 +60,11 @@ constexpr int kMaxSplitTiles = 256;
 constexpr size_t kCounterBytes = kMaxSplitTiles * 4;
 // one part's partial sums of one tile: 32 rows x 128 columns of fp32 per M tile
 constexpr size_t kPartTileBytes = 32 * kCols * 4;
+// partial sums start past every GEMM's counter words (qsplit.h)
+constexpr size_t kPartBase = split::kPartOffset;
+static_assert(kCounterBytes <= split::kSkCounterBytes, "split-K counters within their workspace words");
 __host__ __device__ constexpr size_t ws_bytes(int S, int M, int N) {
-    return S > 1 ? kCounterBytes + (size_t)S * ((N + kCols - 1) / kCols) * ((M + 31) / 32) * kPartTileBytes : 0;
+    return S > 1 ? kPartBase + (size_t)S * ((N + kCols - 1) / kCols) * ((M + 31) / 32) * kPartTileBytes : 0;
 }
 // buffer cache policy of the partials: device scope (sc1)
 constexpr int kCachePolicyDevice = 16;
@@ -295,7 +299,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qgemm_sk_kernel(
     // 64 lanes x 16 bytes, so each lane moves 16-byte vectors.
     const int tiles = (int)gridDim.x / S;
     uint32_t* counters = static_cast<uint32_t*>(ws);
-    const auto pr = rsrc(static_cast<uint8_t*>(ws) + kCounterBytes, (uint32_t)((size_t)tiles * S * MT * kPartTileBytes));
+    const auto pr = rsrc(static_cast<uint8_t*>(ws) + kPartBase, (uint32_t)((size_t)tiles * S * MT * kPartTileBytes));
     auto part_off = [&](int q_part, int t, int q) {
         return (uint32_t)(((size_t)(tile * S + q_part) * MT + t) * kPartTileBytes) + (uint32_t)((q * kWaves + wave) * 1024 + lane * 16);
     };

@@ -25,6 +25,9 @@ std::mutex g_mu;
 // device address of this device's `scratch` (the array's name in host code
 // is a host-side stand-in, not a device address); null until set up
 void* g_scratch[kMaxDevices] = {nullptr};
+// launches on each device's scratch so far (the GEMMs' split tiles meet by
+// this launch number, never 0)
+uint32_t g_epoch[kMaxDevices] = {0};
 
 __global__ void clear_words(uint32_t* p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -37,7 +40,7 @@ __global__ void clear_words(uint32_t* p, size_t n) {
 // That first call must not be under stream capture: the clear would become
 // a node of the caller's graph and run on every replay, after later calls
 // have relied on the array being clear once.  It is refused instead.
-LuxBackendError scratch_on(int dev, hipStream_t st, void** out) {
+LuxBackendError scratch_on(int dev, hipStream_t st, void** out, uint32_t* epoch) {
     std::lock_guard<std::mutex> lock(g_mu);
     if (g_scratch[dev] == nullptr) {
         if (!lux_hip_is_gfx950(dev)) return LUX_BACKEND_ERROR_NOT_SUPPORTED;
@@ -59,6 +62,8 @@ LuxBackendError scratch_on(int dev, hipStream_t st, void** out) {
         g_scratch[dev] = p;
     }
     *out = g_scratch[dev];
+    if (++g_epoch[dev] == 0u) g_epoch[dev] = 1u;
+    *epoch = g_epoch[dev];
     return LUX_BACKEND_OK;
 }
 
@@ -80,7 +85,8 @@ extern "C" __attribute__((visibility("default"))) LuxBackendError lux_gpu_quanti
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LUX_BACKEND_ERROR_DEVICE_LOST;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     void* ws = nullptr;
-    e = scratch_on(dev, st, &ws);
+    uint32_t epoch = 0;
+    e = scratch_on(dev, st, &ws, &epoch);
     if (e != LUX_BACKEND_OK) return e;
 
     lxq::QmmArgs a;
@@ -93,5 +99,6 @@ extern "C" __attribute__((visibility("default"))) LuxBackendError lux_gpu_quanti
     a.x_dtype = x_dtype; a.sb_dtype = sb_dtype; a.out_dtype = out_dtype;
     a.ws = ws;
     a.ws_bytes = lxq::kSplitWorkspaceBytes;
+    a.epoch = epoch;
     return lux_hip_qmm_dispatch(a, kernel, st);
 }

@@ -422,8 +422,9 @@ def test_gemm_parity(ctx, oracle, bits, xd, sbd, od):
     for (M, K, N, gs) in [(300, 512, 200, 64), (256, 1024, 128, 32), (33, 256, 130, 128),
                           (512, 768, 384, 64)]:
         x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 17 + M)
-        if sbd == F32 and gs == 32 and bits >= 6:
+        if sbd == F32 and gs == 32 and bits >= 6 and not (bits == 8 and K % 1024 == 0):
             # the GEMM's LDS buffers do not fit one CU for this combination
+            # (the register-W kernel takes 8-bit codes with K % 1024 == 0)
             with pytest.raises(runtime.LuxError) as e:
                 run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
             assert e.value.code == abi.ERR_NOT_SUPPORTED
@@ -432,6 +433,26 @@ def test_gemm_parity(ctx, oracle, bits, xd, sbd, od):
         y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
         want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, w_round=xd)
         check_output(O, y, want, od, f"gemm b{bits} M{M} K{K} N{N} g{gs}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("xd,sbd,od", [(BF16, BF16, BF16), (F16, F16, F16), (BF16, F32, F32),
+                                       (F16, BF16, F32)])
+def test_rw_gemm_parity(ctx, oracle, bits, gs, xd, sbd, od):
+    """M > 64, 4/8-bit codes, K % 1024 == 0: the register-W GEMM (128 x 256
+    tiles, each wave dequantizing its own columns' codes into its MFMA
+    operand).  Against the oracle's dequantize-to-T form: ragged M and N
+    (tile edges, rows and columns past the ends), a shape whose 128 tiles all
+    run as two K halves meeting in the workspace, and one on the XCD-grouped
+    tile order (16 x 16 tiles)."""
+    O = oracle
+    for (M, K, N) in [(300, 1024, 200), (513, 2048, 520), (1024, 2048, 4096), (2048, 1024, 4096)]:
+        print(f"[case] rw gemm b{bits} g{gs} x{xd} s{sbd} o{od} M{M} K{K} N{N}", flush=True)
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=bits * 31 + M + gs)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, variant="omp", w_round=xd)
+        check_output(O, y, want, od, f"rw gemm b{bits} g{gs} M{M} K{K} N{N}")
 
 
 @pytest.mark.parametrize("bits", BITS)
@@ -713,6 +734,8 @@ def test_fused_errors(ctx, oracle):
 
 @pytest.mark.parametrize("M,K,N,bits,gs,xd,sbd,kern", [
     (96, 512, 136, 4, 64, BF16, BF16, "gemm"),   # large GEMM
+    (200, 1024, 300, 4, 64, BF16, BF16, "gemm"), # register-W large GEMM
+    (130, 2048, 264, 8, 128, F16, F32, "gemm"),  # register-W large GEMM, 8-bit
     (32, 1024, 70, 3, 32, F16, F32, "gemm"),     # small-M GEMM
     (24, 1152, 300, 4, 64, BF16, BF16, "gemm"),  # split-K small-M GEMM (3 K parts)
     (1, 4096, 96, 4, 64, F16, F16, "gemv"),      # whole-line GEMV
