@@ -83,7 +83,7 @@ size_t qgemm_sk_workspace(int M, int K, int N, int bits, int x_dtype, size_t cap
 // and the large GEMM's split last round (at most 128 tiles, one K half of
 // 128 KiB each).  The first KiB holds tile counters and flags.
 constexpr size_t kSplitWorkspaceBytes = (16u << 20) + 4096;
-// MFMA GEMM for large M with each wave's W operand dequantized in its own
+// MFMA GEMM for M > 64 with each wave's W operand dequantized in its own
 // registers: 4/8-bit codes, f16/bf16 x, K % 1024 == 0; NotSupported otherwise
 LuxStatus launch_qgemm_rw(const QmmArgs& a, hipStream_t st);
 // MFMA GEMM for f16/bf16 activations; needs K % 64 == 0

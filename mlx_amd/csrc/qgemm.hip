@@ -7,21 +7,21 @@
 namespace lxq {
 
 LuxStatus launch_qgemm(const QmmArgs& a, hipStream_t st) {
-    // 8 < M <= 64: the split-K small-M kernel, else the W-streaming one
-    if (a.M <= 64) {
-        LuxStatus s = launch_qgemm_sk(a, st);
-        if (s != LuxStatus::NotSupported) return s;
-        s = launch_qgemm_small(a, st);
-        if (s != LuxStatus::NotSupported) return s;
-    }
-    // 4/8-bit codes with K % 1024 == 0: the register-W kernel (unless
-    // LUX_HIP_GEMM_RW=0 asks for the LDS-dequant kernel below)
+    // M > 64 with 4/8-bit codes and K % 1024 == 0: the register-W kernel
+    // (unless LUX_HIP_GEMM_RW=0 asks for the kernels below)
     static const bool rw_on = [] {
         const char* e = std::getenv("LUX_HIP_GEMM_RW");
         return !(e && e[0] == '0');
     }();
     if (rw_on) {
         const LuxStatus s = launch_qgemm_rw(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+    }
+    // 8 < M <= 64: the split-K small-M kernel, else the W-streaming one
+    if (a.M <= 64) {
+        LuxStatus s = launch_qgemm_sk(a, st);
+        if (s != LuxStatus::NotSupported) return s;
+        s = launch_qgemm_small(a, st);
         if (s != LuxStatus::NotSupported) return s;
     }
     // the scale windows cover 4 K steps of 64 codes

@@ -64,23 +64,28 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 256, BK = 64;
-constexpr int kXStage = BM * BK * 2;  // 16 KiB
-constexpr int kSS = 3;                // scale windows
+constexpr int BN = 256, BK = 64;
 constexpr int kCUs = 256;
 
-template <int TX_, int BITS_, int SB_, int GS_, int NW_, int D_, int BAR_>
+template <int TX_, int BITS_, int SB_, int GS_, int NW_, int D_, int BAR_, int MT_>
 struct Cfg {
     static constexpr int TX = TX_, BITS = BITS_, SB = SB_, GS = GS_, NW = NW_;
+    static constexpr int MT = MT_;                 // 32-row M tiles per block
+    static constexpr int BM = 32 * MT;
+    static constexpr int kXStage = BM * BK * 2;    // one K step of the block's x rows
     static constexpr int D = D_;                   // K steps of transfers in flight
     static constexpr int BAR = BAR_;               // K steps per barrier
     static constexpr int kSb = SB == DT_F32 ? 4 : 2;
     static constexpr int kThreads = 64 * NW;
     static constexpr int WN = BN / NW;             // columns per wave
     static constexpr int NT = WN / 32;             // 32-column tiles per wave
-    static constexpr int kXI = 16 / NW;            // x transfers (1 KiB) per wave per step
+    // x transfers per wave per step (whole 1 KiB ones, or one with the
+    // first kXL lanes where the stage is smaller than a transfer per wave)
+    static constexpr int kXI = MT * 4 >= NW ? MT * 4 / NW : 1;
+    static constexpr int kXL = MT * 4 >= NW ? 64 : 64 * MT * 4 / NW;
     static constexpr int kCI = NT * BITS / 4;      // code transfers per wave per step
     static constexpr int kWS = GS / (4 * kSb);     // K steps per scale window
+    static constexpr int kSS = 1 + (D + kWS - 1) / kWS < 3 ? 3 : 1 + (D + kWS - 1) / kWS;  // scale windows
     static constexpr int kSI = NW == 4 ? 2 : 1;    // scale transfers per wave per window
     static constexpr int kXS = D + BAR;            // x stages
     static constexpr int kCS = D + 1;              // code stages
@@ -96,6 +101,7 @@ struct Cfg {
     static_assert((kSS - 1) * kWS >= D, "a scale window slot is refilled only after its last read");
     static_assert(kLds <= 160 * 1024, "LDS budget");
     static_assert(kLds >= BM * (BN * 2 + 16) && kLds >= BM / 2 * (BN * 4 + 16), "the output tile's LDS passes fit");
+    static_assert(MT == 1 || MT == 2 || MT == 4, "32, 64 or 128 rows per block");
     // transfers of the batch of step k (k % kUnroll == p)
     static constexpr int batch(int p) { return kXI + kCI + (p % kWS == 0 ? kSI : 0); }
     // transfers a step (k % kUnroll == P) may leave in flight when it waits:
@@ -230,10 +236,12 @@ __device__ __forceinline__ void issue(const Ctx<C>& t, int kt) {
     const int k = kt < t.KT ? kt : t.KT - 1;
     const int xs = kt % C::kXS, cs = kt % C::kCS;
     {
-        const uint32_t base = t.lds_addr + (uint32_t)(xs * kXStage) + (uint32_t)(t.wave * C::kXI * 1024);
+        const uint32_t base = t.lds_addr + (uint32_t)(xs * C::kXStage) + (uint32_t)(t.wave * C::kXI * C::kXL * 16);
         const uint8_t* src = t.x + (size_t)k * (BK * 2);
+        if (C::kXL == 64 || t.lane < C::kXL) {
 #pragma unroll
-        for (int i = 0; i < C::kXI; i++) dma16(base + 1024u * i, src, t.xoff[i]);
+            for (int i = 0; i < C::kXI; i++) dma16(base + (uint32_t)(C::kXL * 16 * i), src, t.xoff[i]);
+        }
     }
     {
         const uint32_t base = t.lds_addr + (uint32_t)(C::kC0 + cs * C::kCodeStage) + (uint32_t)(t.wave * C::kCI * 1024);
@@ -243,7 +251,7 @@ __device__ __forceinline__ void issue(const Ctx<C>& t, int kt) {
     }
     if constexpr (WIN) {
         const int win = k / C::kWS;
-        const uint32_t base = t.lds_addr + (uint32_t)(C::kS0 + (kt / C::kWS) % kSS * C::kWinSlot) +
+        const uint32_t base = t.lds_addr + (uint32_t)(C::kS0 + (kt / C::kWS) % C::kSS * C::kWinSlot) +
                               (uint32_t)(t.wave * C::WN * 32);
 #pragma unroll
         for (int i = 0; i < C::kSI; i++) dma16a(base + 1024u * i, t.sp[i] + (size_t)win * 16);
@@ -253,8 +261,8 @@ __device__ __forceinline__ void issue(const Ctx<C>& t, int kt) {
 // registers carried from one K step to the next
 template <class C>
 struct Regs {
-    u4 a[4];                      // A fragments of sub-step 0 of the current step (reads in flight)
-    u4 a3[4];                     // A fragments of sub-step 3 of the previous step
+    u4 a[C::MT];                  // A fragments of sub-step 0 of the current step (reads in flight)
+    u4 a3[C::MT];                 // A fragments of sub-step 3 of the previous step
     u4 b3[C::NT];                 // B operands of sub-step 3 of the previous step
     uint32_t cw[C::NT][C::BITS];  // codes of the current step (the lane's 4 BITS bytes per tile)
     SB2 f[C::NT];                 // scale factors of the current step
@@ -274,7 +282,7 @@ __device__ __forceinline__ void read_step(const Ctx<C>& t, int kt, uint32_t (&cw
         }
     // group of the lane's codes within the window: ((kt % kWS) 64 + 32 h) / GS
     const int gi = ((kt % C::kWS) * 64 + 32 * (t.lane >> 5)) / C::GS;
-    const uint8_t* win = t.lds + C::kS0 + (kt / C::kWS) % kSS * C::kWinSlot + gi * C::kSb;
+    const uint8_t* win = t.lds + C::kS0 + (kt / C::kWS) % C::kSS * C::kWinSlot + gi * C::kSb;
 #pragma unroll
     for (int tt = 0; tt < C::NT; tt++) {
         const uint8_t* p = win + t.sb_lds[tt];
@@ -304,18 +312,18 @@ __device__ __forceinline__ void factors(const uint32_t (&rs)[NT], const uint32_t
 
 // A fragments of sub-step j of the x stage of step kt
 template <class C>
-__device__ __forceinline__ void read_a(const Ctx<C>& t, int kt, int j, u4 (&a)[4]) {
-    const uint8_t* X = t.lds + (kt % C::kXS) * kXStage + t.frag;
+__device__ __forceinline__ void read_a(const Ctx<C>& t, int kt, int j, u4 (&a)[C::MT]) {
+    const uint8_t* X = t.lds + (kt % C::kXS) * C::kXStage + t.frag;
     const int off = (((4 * (t.lane >> 5) + j) ^ t.sw) << 4);
 #pragma unroll
-    for (int i = 0; i < 4; i++) a[i] = *reinterpret_cast<const u4*>(X + i * 32 * 128 + off);
+    for (int i = 0; i < C::MT; i++) a[i] = *reinterpret_cast<const u4*>(X + i * 32 * 128 + off);
 }
 
-// the 4 x NT MFMAs of one sub-step
-template <int TX, int NT>
-__device__ __forceinline__ void mfmas(f32x16 (&acc)[4][NT], const u4 (&a)[4], const u4 (&b)[NT]) {
+// the MT x NT MFMAs of one sub-step
+template <int TX, int MT, int NT>
+__device__ __forceinline__ void mfmas(f32x16 (&acc)[MT][NT], const u4 (&a)[MT], const u4 (&b)[NT]) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int tt = 0; tt < NT; tt++) acc[i][tt] = mfma<TX>(a[i], b[tt], acc[i][tt]);
 }
@@ -349,19 +357,19 @@ __device__ __forceinline__ void phase() {
 // barrier step, those of kt + 1 .. kt + BAR), kt + 1's codes and scales.
 // At the end: the barrier (every BAR steps) and kt + 1's first fragments.
 template <class C, int P>
-__device__ __forceinline__ void step(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[4][C::NT], int kt) {
-    constexpr int NT = C::NT, TX = C::TX, BITS = C::BITS;
-    constexpr int V = (BITS == 4 ? 17 : 18) / 4 + 1;  // VALU per MFMA of a B-operand build
+__device__ __forceinline__ void step(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[C::MT][C::NT], int kt) {
+    constexpr int NT = C::NT, TX = C::TX, BITS = C::BITS, MT = C::MT;
+    constexpr int V = (BITS == 4 ? 17 : 18) / MT + 1;  // VALU per MFMA of a B-operand build
     constexpr bool kBarrier = (P + 1) % C::BAR == 0;
     issue<C, (P + C::D) % C::kWS == 0>(t, kt + C::D);
     u4 b[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) b[tt] = b_operand<BITS, TX>(r.cw[tt], 0, r.f[tt]);
-    mfmas<TX, NT>(acc, r.a3, r.b3);
+    mfmas<TX, MT, NT>(acc, r.a3, r.b3);
     uint32_t cwn[NT][BITS], rs[NT], rb[NT];
 #pragma unroll
     for (int j = 0; j < 3; j++) {
-        u4 an[4], bn[NT];
+        u4 an[MT], bn[NT];
         read_a(t, kt, j + 1, an);
         if (j == 2) {
             wait_vm<C::young(P)>();
@@ -369,9 +377,9 @@ __device__ __forceinline__ void step(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[
         }
 #pragma unroll
         for (int tt = 0; tt < NT; tt++) bn[tt] = b_operand<BITS, TX>(r.cw[tt], j + 1, r.f[tt]);
-        mfmas<TX, NT>(acc, j == 0 ? r.a : r.a3, b);
+        mfmas<TX, MT, NT>(acc, j == 0 ? r.a : r.a3, b);
 #pragma unroll
-        for (int i = 0; i < 4; i++) r.a3[i] = an[i];
+        for (int i = 0; i < MT; i++) r.a3[i] = an[i];
 #pragma unroll
         for (int tt = 0; tt < NT; tt++) b[tt] = bn[tt];
     }
@@ -386,10 +394,10 @@ __device__ __forceinline__ void step(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[
     // fragment reads of the next sub-step first, then each MFMA followed by
     // a share of the VALU that builds the next B operands
     constexpr int kDsExtra = NT * (BITS / 4) + 2 * NT;  // codes and scale reads of kt + 1
-    phase<4, 4 * NT, V>();
-    phase<4, 4 * NT, V>();
-    phase<4, 4 * NT, V>();
-    phase<4 + kDsExtra, 4 * NT, V>();
+    phase<MT, MT * NT, V>();
+    phase<MT, MT * NT, V>();
+    phase<MT, MT * NT, V>();
+    phase<MT + kDsExtra, MT * NT, V>();
     wait_lgkm0();
     if constexpr (kBarrier) barrier();
     else __builtin_amdgcn_sched_barrier(0);
@@ -397,7 +405,7 @@ __device__ __forceinline__ void step(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[
 }
 
 template <class C, int P>
-__device__ __forceinline__ void steps(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[4][C::NT], int kt) {
+__device__ __forceinline__ void steps(const Ctx<C>& t, Regs<C>& r, f32x16 (&acc)[C::MT][C::NT], int kt) {
     if constexpr (P < C::kUnroll) {
         step<C, P>(t, r, acc, kt + P);
         steps<C, P + 1>(t, r, acc, kt);
@@ -412,26 +420,36 @@ __device__ __forceinline__ void prologue_issue(const Ctx<C>& t) {
     }
 }
 
-// what one work unit is: a whole tile, or one K half of a tile of the split
-// last round; its M / N tile (XCD-grouped order) and K steps
+// what one work unit is: a whole tile, one K half of a tile of the split
+// last round, or one of nsplit K parts; its M / N tile and K steps
 struct Unit {
     int tile, part, KT, k0, m0, n0;
 };
 
-__device__ __forceinline__ Unit unit_of(int u, int tiles, int split_from, int mtiles, int ntiles, int KT) {
+template <class C>
+__device__ __forceinline__ Unit unit_of(int u, int tiles, int split_from, int nsplit, int mtiles, int ntiles,
+                                        int KT) {
     Unit w;
     w.tile = u;
     w.part = -1;
     w.KT = KT;
-    // units below split_from are whole tiles; the rest are the two K halves
-    // (all first halves, then all second halves) of tiles split_from ..
-    if (u >= split_from) {
+    w.k0 = 0;
+    if (nsplit > 1) {
+        // K parts: unit u = part * tiles + tile (the blocks running together
+        // share a K range, i.e. the same x columns)
+        w.tile = u % tiles;
+        w.part = u / tiles;
+        w.KT = KT / nsplit;
+        w.k0 = w.part * w.KT;
+    } else if (u >= split_from) {
+        // units below split_from are whole tiles; the rest are the two K
+        // halves (all first halves, then all second halves) of tiles split_from ..
         const int r = tiles - split_from, i = u - split_from;
         w.part = i >= r;
         w.tile = split_from + i - w.part * r;
         w.KT = KT >> 1;
+        w.k0 = w.part * w.KT;
     }
-    w.k0 = w.part > 0 ? w.KT : 0;
     // tile -> (M tile, N tile): groups of 256 tiles, 32 per XCD as 4 x 8
     // M x N tiles, where the shape has whole groups; the rest in order
     const int tile = w.tile;
@@ -448,7 +466,7 @@ __device__ __forceinline__ Unit unit_of(int u, int tiles, int split_from, int mt
         mt = r % mtiles;
         nt = n_done + r / mtiles;
     }
-    w.m0 = mt * BM;
+    w.m0 = mt * C::BM;
     w.n0 = nt * BN;
     return w;
 }
@@ -458,15 +476,15 @@ template <class C, bool EPI>
 __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep, int mtiles,
-    int ntiles, int split_from, void* __restrict__ ws, uint32_t epoch) {
-    constexpr int NT = C::NT, BITS = C::BITS, NW = C::NW, GS = C::GS;
+    int ntiles, int split_from, int nsplit, void* __restrict__ ws, uint32_t epoch) {
+    constexpr int NT = C::NT, BITS = C::BITS, NW = C::NW, GS = C::GS, MT = C::MT, BM = C::BM;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, h = lane >> 5;
     const int tiles = mtiles * ntiles;
 
-    const Unit w = unit_of(blockIdx.x, tiles, split_from, mtiles, ntiles, K / BK);
+    const Unit w = unit_of<C>(blockIdx.x, tiles, split_from, nsplit, mtiles, ntiles, K / BK);
     const int m0 = w.m0, n0 = w.n0, k0 = w.k0;
 
     Ctx<C> t;
@@ -477,13 +495,14 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     t.wave = wave;
     t.lane = lane;
     t.KT = w.KT;
-    // x transfers: wave w, transfer i fills 1 KiB block q = w kXI + i = rows
-    // 8 q .. 8 q + 7; lane -> row 8 q + lane / 8, LDS chunk lane % 8, which
-    // holds global chunk (lane % 8) ^ swz(row)
+    // x transfers: wave w, transfer i fills the kXL * 16 bytes from block q
+    // = w kXI + i on, 8 lanes per 128-byte row: lane -> row q kXL / 8 +
+    // lane / 8, LDS chunk lane % 8, which holds global chunk (lane % 8) ^
+    // swz(row)
 #pragma unroll
     for (int i = 0; i < C::kXI; i++) {
-        const int row = 8 * (wave * C::kXI + i) + (lane >> 3);
-        const int rg = min(m0 + row, M - 1);  // rows past M: valid data, never stored
+        const int row = (wave * C::kXI + i) * (C::kXL / 8) + (lane >> 3);
+        const int rg = min(m0 + min(row, BM - 1), M - 1);  // rows past M: valid data, never stored
         t.xoff[i] = ((uint32_t)rg * (uint32_t)K + (uint32_t)(((lane & 7) ^ swz(row)) << 3)) * 2u;
     }
     // code transfers: tile tt, part e: column n0 + w WN + 32 tt + c, the 16
@@ -513,9 +532,9 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) t.sb_lds[tt] = wave * C::WN * 32 + (32 * tt + c) * 16;
 
-    f32x16 acc[4][NT];
+    f32x16 acc[MT][NT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int tt = 0; tt < NT; tt++)
 #pragma unroll
@@ -526,7 +545,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     // MFMAs add +0 to the +0 accumulators)
     Regs<C> r;
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.a3[i] = u4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < MT; i++) r.a3[i] = u4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) r.b3[tt] = u4{0u, 0u, 0u, 0u};
     prologue_issue<C, 0>(t);
@@ -546,28 +565,85 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     }
     read_a(t, 0, 0, r.a);
 
-    // KT is a multiple of kUnroll (K % 1024 == 0; halves: (K / 128) % kUnroll == 0)
+    // KT is a multiple of kUnroll (the launcher's split rules keep it so)
     for (int kt = 0; kt < w.KT; kt += C::kUnroll) steps<C, 0>(t, r, acc, kt);
     // sub-step 3 of the last step
-    mfmas<C::TX, NT>(acc, r.a3, r.b3);
+    mfmas<C::TX, MT, NT>(acc, r.a3, r.b3);
     // no transfer may still be landing when LDS is next written
     wait_vm<0>();
 
-    if (w.part >= 0) {
-        // ---- split tile: the two K halves meet (qsplit.h) ----
+    // a thread's sums as 16-byte vectors q (q = (i NT + tt) 4 + v / 4):
+    // vector q of thread tid at byte (q threads + tid) 16 of a partial slot
+    constexpr int kVec = MT * NT * 4;
+    constexpr uint32_t kSlot = (uint32_t)(kVec * C::kThreads * 16);  // = BM BN 4
+    const uint32_t voff = (uint32_t)tid * 16u;
+    uint32_t* word = reinterpret_cast<uint32_t*>(lds);  // every transfer has landed
+    if (nsplit > 1) {
+        // ---- K parts: every part stores its sums; the last to count in adds
+        // all nsplit of them in part order (the same bits whichever part is
+        // last) and stores y; it also returns the tile's counter to zero ----
+        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+            static_cast<uint8_t*>(ws) + split::kPartOffset, 0, (int)((uint32_t)(tiles * nsplit) * kSlot), 0x00020000);
+        const uint32_t slot = (uint32_t)(w.tile * nsplit + w.part) * kSlot;
+#pragma unroll
+        for (int q = 0; q < kVec; q++) {
+            const f32x16& a = acc[q / (4 * NT)][(q / 4) % NT];
+            const int v = 4 * (q % 4);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u4{__float_as_uint(a[v]), __float_as_uint(a[v + 1]), __float_as_uint(a[v + 2]), __float_as_uint(a[v + 3])},
+                pr, voff, slot + (uint32_t)q * (C::kThreads * 16u), split::kCachePolicyDevice);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        barrier();
+        if (tid == 0) *word = split::count_part(ws, w.tile, nsplit) ? 1u : 0u;
+        barrier();
+        if (*word == 0u) return;
+        const uint32_t first = (uint32_t)(w.tile * nsplit) * kSlot;
+#pragma unroll
+        for (int q = 0; q < kVec; q++) {
+            f32x16& a = acc[q / (4 * NT)][(q / 4) % NT];
+            const int v = 4 * (q % 4);
+            a[v] = a[v + 1] = a[v + 2] = a[v + 3] = 0.f;
+        }
+        // kPB parts' sums in flight together (32 vectors per thread: one
+        // memory round trip per kPB parts, not per part); nsplit is a power
+        // of two, so whole batches or a single one
+        constexpr int kPB = kVec >= 32 ? 1 : 32 / kVec;
+        for (int p0 = 0; p0 < nsplit; p0 += kPB) {
+            u4 o[kPB][kVec];
+#pragma unroll
+            for (int pp = 0; pp < kPB; pp++)
+#pragma unroll
+                for (int q = 0; q < kVec; q++)
+                    o[pp][q] = p0 + pp < nsplit
+                                   ? __builtin_amdgcn_raw_buffer_load_b128(
+                                         pr, voff, first + (uint32_t)(p0 + pp) * kSlot + (uint32_t)q * (C::kThreads * 16u),
+                                         split::kCachePolicyDevice)
+                                   : u4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int pp = 0; pp < kPB; pp++) {
+                if (p0 + pp >= nsplit) break;
+#pragma unroll
+                for (int q = 0; q < kVec; q++) {
+                    f32x16& a = acc[q / (4 * NT)][(q / 4) % NT];
+                    const int v = 4 * (q % 4);
+                    a[v] += __uint_as_float(o[pp][q].x);
+                    a[v + 1] += __uint_as_float(o[pp][q].y);
+                    a[v + 2] += __uint_as_float(o[pp][q].z);
+                    a[v + 3] += __uint_as_float(o[pp][q].w);
+                }
+            }
+        }
+    } else if (w.part >= 0) {
+        // ---- split last round: the two K halves meet (qsplit.h) ----
         const int st = w.tile - split_from;
         const uint32_t nslots = (uint32_t)(tiles - split_from);
         const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-            static_cast<uint8_t*>(ws) + split::kPartOffset, 0, (int)(nslots * (uint32_t)(BM * BN * 4)), 0x00020000);
-        // a thread's sums as 16-byte vectors q: vector q of thread tid at
-        // byte ((st kVec + q) threads + tid) 16 of the partial sums
-        const uint32_t voff = (uint32_t)tid * 16u;
-        uint32_t* word = reinterpret_cast<uint32_t*>(lds);  // every transfer has landed
+            static_cast<uint8_t*>(ws) + split::kPartOffset, 0, (int)(nslots * kSlot), 0x00020000);
         barrier();
         if (tid == 0) *word = split::arrive_first(ws, st) ? 1u : 0u;
         barrier();
-        constexpr int kVec = 4 * NT * 4;
-        const uint32_t slot = (uint32_t)st * (uint32_t)(kVec * C::kThreads * 16);
+        const uint32_t slot = (uint32_t)st * kSlot;
         if (*word == 1u) {
 #pragma unroll
             for (int q = 0; q < kVec; q++) {
@@ -602,18 +678,18 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     // ---- output: lane holds column c of each 32 x 32 tile, VGPR v row
     // 8 (v / 4) + 4 h + v % 4.  The tile goes through LDS (free now: every
     // transfer has landed and every wave is past the K loop at the barrier)
-    // so that the stores to y are whole 16-byte chunks of rows: 16-bit
-    // outputs in one pass of the 128 rows, fp32 outputs in two passes of 64.
+    // so that the stores to y are whole 16-byte chunks of rows, in one pass
+    // (two of half the rows for fp32 outputs of 128-row tiles).
     const bool f32_out = ep.out_dt == DT_F32;
     const int esz = f32_out ? 4 : 2;
     const int rs = BN * esz + 16;  // LDS row stride: rows m and m + 4 in different banks
     // vector stores need 16-byte aligned rows: N a multiple of 16 / esz, y aligned
     const bool vec = (((uintptr_t)y) & 15) == 0 && (N % (16 / esz)) == 0;
-    const int passes = f32_out ? 2 : 1, prow = BM / passes;
+    const int passes = BM * rs > C::kLds ? 2 : 1, prow = BM / passes;
     for (int ps = 0; ps < passes; ps++) {
         barrier();
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < MT; i++) {
             if (i * 32 / prow != ps) continue;
 #pragma unroll
             for (int tt = 0; tt < NT; tt++) {
@@ -664,37 +740,61 @@ inline bool applies(int M, int K, int N, int bits, int x_dtype) {
            N > 0 && (size_t)M * K * 2 < (1ull << 32) && (size_t)N * K * bits / 8 < (1ull << 32);
 }
 
+// K parts for a shape with few tiles: the largest power of two (at most 16)
+// that keeps the grid within one block per CU, every part a whole number of
+// unrolled loops, and the parts' sums within the workspace; 1 for shapes
+// with at least half a round of tiles (their last round splits instead)
+template <class C>
+inline int k_parts(int tiles, int KT, const QmmArgs& a) {
+    if (a.ws == nullptr || 2 * tiles > kCUs || tiles > split::kMaxPartTiles) return 1;
+    int S = 1;
+    while (S < 16 && tiles * 2 * S <= kCUs && KT % (2 * S * C::kUnroll) == 0 &&
+           split::kPartOffset + (size_t)tiles * 2 * S * C::BM * BN * 4 <= a.ws_bytes)
+        S *= 2;
+    return S;
+}
+
 template <class C, bool EPI>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     auto kern = qgemm_rw_kernel<C, EPI>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
     if (attr != hipSuccess) return LuxStatus::Internal;
-    const int mtiles = (a.M + BM - 1) / BM, ntiles = (a.N + BN - 1) / BN;
-    const int tiles = mtiles * ntiles;
-    // the last round's tiles in two K halves where that round is at most
-    // half full (each half a whole number of unrolled loops)
+    const int mtiles = (a.M + C::BM - 1) / C::BM, ntiles = (a.N + BN - 1) / BN;
+    const int tiles = mtiles * ntiles, KT = a.K / BK;
+    const int nsplit = k_parts<C>(tiles, KT, a);
+    // with whole tiles: the last round's tiles in two K halves where that
+    // round is at most half full (each half a whole number of unrolled loops)
     const int r = tiles % kCUs;
-    const int split_from = a.ws != nullptr && a.epoch != 0u && r > 0 && 2 * r <= kCUs &&
-                                   r <= split::kMaxHalfTiles && (a.K / BK / 2) % C::kUnroll == 0 &&
-                                   a.ws_bytes >= split::kPartOffset + (size_t)r * (BM * BN * 4)
+    const int split_from = nsplit == 1 && a.ws != nullptr && a.epoch != 0u && r > 0 && 2 * r <= kCUs &&
+                                   r <= split::kMaxHalfTiles && (KT / 2) % C::kUnroll == 0 &&
+                                   a.ws_bytes >= split::kPartOffset + (size_t)r * (C::BM * BN * 4)
                                ? tiles - r
                                : tiles;
-    hipLaunchKernelGGL(kern, dim3(tiles + (tiles - split_from)), dim3(C::kThreads), C::kLds, st,
-                       static_cast<const uint16_t*>(a.x), a.wq, a.scales, a.biases, a.y, a.M, a.K, a.N, a.epi(),
-                       mtiles, ntiles, split_from, a.ws, a.epoch);
+    const int blocks = nsplit > 1 ? tiles * nsplit : tiles + (tiles - split_from);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(C::kThreads), C::kLds, st, static_cast<const uint16_t*>(a.x), a.wq,
+                       a.scales, a.biases, a.y, a.M, a.K, a.N, a.epi(), mtiles, ntiles, split_from, nsplit, a.ws,
+                       a.epoch);
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 
-template <class C>
-LuxStatus launch_c(const QmmArgs& a, hipStream_t st) {
-    return a.has_epilogue() ? launch_e<C, true>(a, st) : launch_e<C, false>(a, st);
-}
+// the configuration the plugin runs: two waves per SIMD, a barrier every
+// step, 3 K steps of transfers in flight (a K step of a 128-row block runs
+// ~0.9 us, so 3 steps ahead cover the memory latency)
+template <int TX, int BITS, int SB, int GS, int MT>
+using PluginCfg = Cfg<TX, BITS, SB, GS, 8, 3, 1, MT>;
 
-// the configuration the plugin runs: two waves per SIMD, 3 K steps of
-// transfers in flight, a barrier every step
+// M > 64 (128-row blocks).  The 32- and 64-row forms of this kernel
+// (MT = 1, 2) measured slower than the small-M GEMMs at every M <= 64 shape
+// tried (c2 25.6 against 21.5 us; M = 17, 32, 64 at N = 8192..14336 by
+// 10-65 %): a K step of so few rows is short, so each CU's transfers in
+// flight bound its stream, and the K-part reduction adds a serial tail.
 template <int TX, int BITS, int SB, int GS>
-using PluginCfg = Cfg<TX, BITS, SB, GS, 8, 3, 1>;
+LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
+    if (a.M <= 64) return LuxStatus::NotSupported;
+    return a.has_epilogue() ? launch_e<PluginCfg<TX, BITS, SB, GS, 4>, true>(a, st)
+                            : launch_e<PluginCfg<TX, BITS, SB, GS, 4>, false>(a, st);
+}
 
 // one activation type and group size (one translation unit each): the code
 // width and scale type
@@ -702,9 +802,9 @@ template <int TX, int GS>
 LuxStatus launch_tg(const QmmArgs& a, hipStream_t st) {
     const bool b8 = a.bits == 8;
     switch (a.sb_dtype) {
-    case DT_F32: return b8 ? launch_c<PluginCfg<TX, 8, DT_F32, GS>>(a, st) : launch_c<PluginCfg<TX, 4, DT_F32, GS>>(a, st);
-    case DT_F16: return b8 ? launch_c<PluginCfg<TX, 8, DT_F16, GS>>(a, st) : launch_c<PluginCfg<TX, 4, DT_F16, GS>>(a, st);
-    default: return b8 ? launch_c<PluginCfg<TX, 8, DT_BF16, GS>>(a, st) : launch_c<PluginCfg<TX, 4, DT_BF16, GS>>(a, st);
+    case DT_F32: return b8 ? launch_m<TX, 8, DT_F32, GS>(a, st) : launch_m<TX, 4, DT_F32, GS>(a, st);
+    case DT_F16: return b8 ? launch_m<TX, 8, DT_F16, GS>(a, st) : launch_m<TX, 4, DT_F16, GS>(a, st);
+    default: return b8 ? launch_m<TX, 8, DT_BF16, GS>(a, st) : launch_m<TX, 4, DT_BF16, GS>(a, st);
     }
 }
 

@@ -8,6 +8,8 @@
 //                        kernel returns each to zero at the end of a launch)
 //   bytes [1024, 1536)   large-GEMM split-tile arrival counters (128 words)
 //   bytes [1536, 2048)   large-GEMM split-tile flags (128 words)
+//   bytes [2048, 3072)   register-W GEMM K-part counters (256 words; the
+//                        last part of a tile returns its counter to zero)
 //   bytes [4096, ...)    partial sums of whichever kernel runs (meaningful
 //                        only within the launch that writes them)
 // The two kernels' words never overlap, so neither can disturb the other's
@@ -37,12 +39,29 @@ constexpr size_t kSkCounterBytes = 1024;
 constexpr int kHalfCounterWord = 256;
 constexpr int kHalfFlagWord = 384;
 constexpr int kMaxHalfTiles = 128;
+constexpr int kPartCounterWord = 512;
+constexpr int kMaxPartTiles = 256;
 constexpr size_t kPartOffset = 4096;
 // cache policy of the workspace accesses: device scope (sc1).  The halves
 // may run on different XCDs, whose L2s are not coherent with each other.
 constexpr int kCachePolicyDevice = 16;
 static_assert(kHalfFlagWord + kMaxHalfTiles <= (int)(kPartOffset / 4), "split words below the partial sums");
 static_assert(kSkCounterBytes <= (size_t)kHalfCounterWord * 4, "split-K counters below the large-GEMM words");
+
+static_assert(kHalfFlagWord + kMaxHalfTiles <= kPartCounterWord &&
+                  (size_t)(kPartCounterWord + kMaxPartTiles) * 4 <= kPartOffset,
+              "K-part counters between the flags and the partial sums");
+
+// K parts (register-W GEMM): one thread per block, after the block's sums
+// are stored (vmcnt(0)) and the block has met at a barrier.  true for the
+// last of the tile's `parts` to count in, which also sets the counter back
+// to zero for the next launch (every other part has counted in by then).
+__device__ __forceinline__ bool count_part(void* ws, int tile, int parts) {
+    uint32_t* c = static_cast<uint32_t*>(ws) + kPartCounterWord + tile;
+    const bool last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(parts - 1);
+    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
 
 // One thread per block.  true: this block is the first of the tile's two
 // halves to arrive (it stores its sums, then publish()es); false: the
