@@ -113,10 +113,12 @@ def test_quant_extension_table_without_gpu():
     assert q.select_kernel(1, 4096, 14336, 64, 4, abi.FLOAT16, abi.FLOAT16) == abi.KERNEL_GEMV
     assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.BFLOAT16, abi.BFLOAT16) == abi.KERNEL_GEMM
     assert q.select_kernel(2048, 4096, 4096, 64, 4, abi.FLOAT32, abi.FLOAT32) == abi.KERNEL_GEMV
-    # K not a multiple of 256, and f32 scales at group 32 with 8-bit codes,
-    # stay on the GEMV
+    # K not a multiple of 256, and f32 scales at group 32 with 8-bit codes
+    # where the register-W GEMM does not apply (K % 1024 != 0), stay on the
+    # GEMV; with K % 1024 == 0 that GEMM takes them
     assert q.select_kernel(2048, 4160, 4096, 64, 4, abi.BFLOAT16, abi.BFLOAT16) == abi.KERNEL_GEMV
-    assert q.select_kernel(2048, 4096, 4096, 32, 8, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMV
+    assert q.select_kernel(2048, 4352, 4096, 32, 8, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMV
+    assert q.select_kernel(2048, 4096, 4096, 32, 8, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMM
     assert q.select_kernel(2048, 4096, 4096, 32, 4, abi.BFLOAT16, abi.FLOAT32) == abi.KERNEL_GEMM
     # the GEMV/GEMM crossover: M = 16 for 4/8-bit codes with K % 1024 == 0
     # and 16-bit x (the GEMV's MFMA kernels), else M = 8
