@@ -480,7 +480,6 @@ def config_legs(ctx, hip, steps, warmup, keep=False):
     weight-byte and flop rates with their roofline fractions.  keep=True
     also returns the c2 run (inputs and output) for the parity check."""
     from mlx_amd import abi
-    names = {abi.KERNEL_GEMV: "gemv", abi.KERNEL_GEMM: "gemm"}
     out, runs = {}, {}
     for name, M, K, N, bits, gs, xd, sbd, od in CONFIG_LEGS:
         wb = weight_bytes(N, K, bits, gs, sbd)
@@ -490,7 +489,7 @@ def config_legs(ctx, hip, steps, warmup, keep=False):
         flops = 2.0 * M * N * K
         key = f"{name}_m{M}_{bits}bit"
         out[key] = {"M": M, "K": K, "N": N, "bits": bits, "group_size": gs,
-                    "kernel": names.get(ctx.select_kernel(M, K, N, gs, bits, xd, sbd), "?"),
+                    "kernel": ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od),
                     "kernel_us_avg": round(t * 1e6, 3), "kernel_us_median": r["per_launch_us"]["median"],
                     "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                     "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
@@ -506,18 +505,16 @@ def sweep(ctx, hip, steps, only=None, table=SWEEP):
     """One line per config: kernel AUTO picks, per-launch time (stream and
     graph replays), weight GB/s and TFLOP/s with their roofline fractions."""
     from mlx_amd import abi
-    names = {abi.KERNEL_GEMV: "gemv", abi.KERNEL_GEMM: "gemm"}
     for name, M, K, N, bits, gs, xd, sbd, od in table:
         if only and name not in only:
             continue
-        kern = ctx.select_kernel(M, K, N, gs, bits, xd, sbd)
         copies = 4 if M >= 256 else copies_for(weight_bytes(N, K, bits, gs, sbd))
         r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, 8, abi.KERNEL_AUTO, copies=copies)
         t = r["event_ms_per_launch"] * 1e-3
         wb = weight_bytes(N, K, bits, gs, sbd)
         flops = 2.0 * M * N * K
         print(json.dumps({"config": name, "M": M, "K": K, "N": N, "bits": bits, "group_size": gs,
-                          "kernel": names.get(kern, str(kern)), "us": round(t * 1e6, 3),
+                          "kernel": ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od), "us": round(t * 1e6, 3),
                           "us_median": r["per_launch_us"]["median"],
                           "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                           "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
@@ -533,7 +530,8 @@ def decode_legs(ctx, hip, K, N, bits, gs, steps, warmup):
     for m in (4, 8):
         r = bench_qmm(ctx, hip, m, K, N, bits, gs, F16, F16, F16, steps, warmup, abi.KERNEL_AUTO)
         t = r["event_ms_per_launch"] * 1e-3
-        out[f"M{m}"] = {"kernel_us_avg": round(t * 1e6, 3), "kernel_us_median": r["per_launch_us"]["median"],
+        out[f"M{m}"] = {"kernel": ctx.kernel_name(m, K, N, gs, bits, F16, F16, F16),
+                        "kernel_us_avg": round(t * 1e6, 3), "kernel_us_median": r["per_launch_us"]["median"],
                         "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                         "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4)}
     return out
@@ -619,7 +617,8 @@ def main():
                            abi.KERNEL_AUTO, copies=4, keep=keep and n == 4096)
             flops = 2.0 * 2048 * 4096 * n
             tf = flops / (rg["event_ms_per_launch"] * 1e-3) / 1e12
-            gemm[f"N{n}"] = {"tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+            gemm[f"N{n}"] = {"kernel": ctx.kernel_name(2048, 4096, n, 64, 4, BF16, BF16, BF16),
+                             "tflops": round(tf, 2), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                              "kernel_us_avg": round(rg["event_ms_per_launch"] * 1e3, 2),
                              "kernel_us_median": rg["per_launch_us"]["median"],
                              "per_launch_us": rg["per_launch_us"],
@@ -653,11 +652,12 @@ def main():
         "data": "synthetic: x~N(0,1) f16; W~N(0,0.02) quantized on the GPU (4-bit, group 64, "
                 "f16 scales/biases); 16 rotated weight copies",
         "config": {"workload": "configs[1] decode GEMV M=1", "M": M, "K": K, "N": N, "bits": bits,
-                   "group_size": gs, "kernel": "gemv", "hbm_pct": round(100 * value / HBM_PEAK_GBS, 2)},
+                   "group_size": gs, "kernel": ctx.kernel_name(M, K, N, gs, bits, F16, F16, F16),
+                   "hbm_pct": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(GEMV_PROFILE),
-                     "kernel": "qgemv_line_kernel", "kernel_us_avg": round(t * 1e6, 3),
+                     "kernel": ctx.kernel_name(M, K, N, gs, bits, F16, F16, F16), "kernel_us_avg": round(t * 1e6, 3),
                      "kernel_us_median": r["per_launch_us"]["median"], "per_launch_us": r["per_launch_us"],
                      "graph_us_per_launch": round(r["graph_ms_per_launch"] * 1e3, 3),
                      "graph_frac": round(wb / r["graph_ms_per_launch"] / 1e6 / HBM_PEAK_GBS, 4),

@@ -222,6 +222,19 @@ __attribute__((visibility("default"))) LuxBackendError lux_gpu_quantized_matmul_
     int group_size, int bits, LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype, LuxBackendDtype out_dtype,
     LuxQuantKernel kernel, void* stream);
 
+/*
+ * The name of the gfx950 kernel that op_quantized_matmul_ex (with a
+ * context) would launch for this shape and kernel choice: for example
+ * "qgemv_line_kernel" or "qgemm_rw_kernel", the kernel names profilers
+ * show.  NULL where the op would return an error for these arguments; ""
+ * where it launches nothing (M or N zero).  The string is static.  No
+ * counterpart in the reference: a host-only query for tests and tuning
+ * tools that makes no device call, so it answers on a machine without a GPU.
+ */
+__attribute__((visibility("default"))) const char* lux_gpu_quantized_matmul_kernel_name(
+    int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype,
+    LuxBackendDtype out_dtype, LuxQuantKernel kernel);
+
 #ifdef __cplusplus
 }
 #endif

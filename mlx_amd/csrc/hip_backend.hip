@@ -656,3 +656,29 @@ extern "C" __attribute__((visibility("default"))) bool lux_gpu_backend_quant_ini
     *out = &g_qvtbl;
     return true;
 }
+
+// a dry run of the dispatch: every launcher records its kernel's name
+// instead of launching (QmmArgs::plan), so no device call is made and the
+// operand pointers, stand-ins here, are never read
+extern "C" __attribute__((visibility("default"))) const char* lux_gpu_quantized_matmul_kernel_name(
+    int M, int K, int N, int group_size, int bits, LuxBackendDtype x_dtype, LuxBackendDtype sb_dtype,
+    LuxBackendDtype out_dtype, LuxQuantKernel kernel) {
+    if (lux_hip_qmm_validate(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype, kernel) != LUX_BACKEND_OK)
+        return nullptr;
+    if (M == 0 || N == 0) return "";
+    static uint8_t stand_in;
+    const char* name = nullptr;
+    lxq::QmmArgs a;
+    a.x = a.scales = a.biases = &stand_in;
+    a.wq = nullptr;
+    a.y = &stand_in;
+    a.M = M; a.K = K; a.N = N; a.group_size = group_size; a.bits = bits;
+    a.x_dtype = x_dtype; a.sb_dtype = sb_dtype; a.out_dtype = out_dtype;
+    // a context's workspace
+    a.ws = &stand_in;
+    a.ws_bytes = lxq::kSplitWorkspaceBytes;
+    a.epoch = 1u;
+    a.plan = &name;
+    if (lux_hip_qmm_dispatch(a, kernel, nullptr) != LUX_BACKEND_OK) return nullptr;
+    return name;
+}

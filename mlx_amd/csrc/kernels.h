@@ -46,11 +46,23 @@ struct QmmArgs {
     // workspace (the large GEMMs' split tiles meet by it, qsplit.h); 0: no
     // split tiles
     uint32_t epoch = 0;
+    // dry run: when set, the launcher that would run stores its kernel's
+    // name here (the first one, where rows run in chunks) and launches
+    // nothing; no device call is made and no pointer is read
+    const char** plan = nullptr;
     Epilogue epi() const { return Epilogue{bias, bias_dtype, act, out_dtype}; }
     // kernels are instantiated with and without the output stage: the plain
     // op runs code with no bias or activation path at all
     bool has_epilogue() const { return bias != nullptr || act != ACT_NONE; }
 };
+
+// every launcher, once it has decided to run `kernel`: true for a dry run
+// (a.plan set), which records the name and returns without launching
+inline bool planned(const QmmArgs& a, const char* kernel) {
+    if (a.plan == nullptr) return false;
+    if (*a.plan == nullptr) *a.plan = kernel;
+    return true;
+}
 
 // bandwidth-bound dequant-GEMV (any M; tuned for M <= 8); needs K % 64 == 0
 LuxStatus launch_qgemv(const QmmArgs& a, hipStream_t st);

@@ -210,6 +210,7 @@ LuxStatus launch_quantize(const void* w, uint32_t* wq, void* scales, void* biase
 LuxStatus launch_qmm_generic(const QmmArgs& a, hipStream_t st) {
     const size_t total = (size_t)a.M * a.N;
     if (total == 0) return LuxStatus::Ok;
+    if (planned(a, "qmm_generic_kernel")) return LuxStatus::Ok;
     hipLaunchKernelGGL(qmm_generic_kernel, dim3(grid_for(total)), dim3(256), 0, st, a.x, a.wq,
                        a.scales, a.biases, a.y, a.M, a.K, a.N, a.group_size, a.bits, a.x_dtype,
                        a.sb_dtype, a.epi());

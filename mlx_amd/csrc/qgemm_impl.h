@@ -667,6 +667,7 @@ LuxStatus launch4_e(const QmmArgs& a, hipStream_t st) {
     if constexpr (!lds_fits<BITS, GS, SB>()) {
         return LuxStatus::NotSupported;
     } else {
+        if (planned(a, "qgemm_kernel")) return LuxStatus::Ok;
         auto kern = qgemm_kernel<TX, BITS, SB, GS, EPI>;
         constexpr size_t lds = lds_bytes<BITS, GS, SB>();
         static const hipError_t attr = hipFuncSetAttribute(

@@ -756,6 +756,7 @@ inline int k_parts(int tiles, int KT, const QmmArgs& a) {
 
 template <class C, bool EPI>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
+    if (planned(a, "qgemm_rw_kernel")) return LuxStatus::Ok;
     auto kern = qgemm_rw_kernel<C, EPI>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);

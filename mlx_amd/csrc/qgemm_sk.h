@@ -377,6 +377,7 @@ template <int BITS, int TX, int SB, int MT, int GS, bool EPI>
 LuxStatus launch_e(const QmmArgs& a, int S, hipStream_t st) {
     static_assert(Lay<MT>::kBytes <= 64 * 1024, "static LDS");
     const int tiles = (a.N + kCols - 1) / kCols;
+    if (planned(a, "qgemm_sk_kernel")) return LuxStatus::Ok;
     hipLaunchKernelGGL((qgemm_sk_kernel<BITS, TX, SB, MT, GS, EPI>), dim3(tiles * S), dim3(64 * kWaves), 0, st, a.x,
                        a.wq, a.scales, a.biases, a.y, a.M, a.K, a.N, S, a.ws, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;

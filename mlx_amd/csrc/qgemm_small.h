@@ -535,6 +535,7 @@ template <int BITS, int TX, int SB, int MT, int NT, int GS, bool EPI>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     using L = Lay<BITS, SB, MT, NT, GS>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
+    if (planned(a, "qgemm_small_kernel")) return LuxStatus::Ok;
     auto kern = qgemm_small_kernel<BITS, TX, SB, MT, NT, GS, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together

@@ -31,6 +31,7 @@ template <int TX, int SB, int GS, bool EPI, int TILES, int KW = 1024>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     const size_t lds = dec_lds_bytes(a.M, a.K, TILES, KW);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
+    if (planned(a, "qgemv_dec_kernel")) return LuxStatus::Ok;
     auto kern = qgemv_dec_kernel<TX, SB, GS, EPI, TILES, KW>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together

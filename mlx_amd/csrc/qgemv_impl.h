@@ -621,6 +621,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qgemv_stream_kernel(
 
 template <int BITS, int TX, int SB, int MR, int R, bool EPI>
 LuxStatus launch_stream_e(const QmmArgs& a, hipStream_t st) {
+    if (planned(a, "qgemv_stream_kernel")) return LuxStatus::Ok;
     const int rows = kStreamWaves * R;
     const int blocks = (a.N + rows - 1) / rows;
     const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
@@ -847,6 +848,7 @@ __global__ __launch_bounds__(64 * kSplitMaxWaves) void qgemv_split_kernel(
 
 template <int BITS, int TX, int SB, int MR, int R, bool TWO, bool EPI>
 LuxStatus launch_split_k(const QmmArgs& a, hipStream_t st, int ks, int pu, size_t lds) {
+    if (planned(a, "qgemv_split_kernel")) return LuxStatus::Ok;
     auto kern = qgemv_split_kernel<BITS, TX, SB, MR, R, TWO, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together
@@ -917,6 +919,7 @@ LuxStatus launch_t_e(const QmmArgs& a, hipStream_t st) {
     if (rpw < RU) rpw = RU;
     const int waves = (a.N + rpw - 1) / rpw;
     const int blocks = (waves + 3) / 4;
+    if (planned(a, "qgemv_kernel")) return LuxStatus::Ok;
     auto kern = qgemv_kernel<BITS, TX, MR, RU, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together

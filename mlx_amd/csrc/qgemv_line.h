@@ -513,6 +513,7 @@ inline int line_sb_loads(int R, int G, int sb_dtype) {
 
 template <int BITS, int TX, int SB, int R, int NI, bool TWO, int SBQ>
 LuxStatus launch_line_k(const QmmArgs& a, hipStream_t st) {
+    if (planned(a, "qgemv_line_kernel")) return LuxStatus::Ok;
     const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
     const int blocks = (a.N + 4 * R - 1) / (4 * R);
     if (a.has_epilogue())

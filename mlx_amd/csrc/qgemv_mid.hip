@@ -8,6 +8,7 @@ template <int BITS, int TX, int SB, int GS, int XR, bool EPI>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     using L = Lay<BITS, SB, GS, XR>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
+    if (planned(a, "qgemv_mid_kernel")) return LuxStatus::Ok;
     auto kern = qgemv_mid_kernel<BITS, TX, SB, GS, XR, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together

@@ -231,6 +231,7 @@ template <int BITS, int TX, int SB, int MX, int RB, int SBQ, int KW>
 LuxStatus launch_mx_k(const QmmArgs& a, hipStream_t st) {
     using L = MxLds<RB, MX, SBQ, KW>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
+    if (planned(a, "qgemv_mx_kernel")) return LuxStatus::Ok;
     if constexpr (L::kBytes > 64 * 1024) {
         // once per instantiation (a function-local static initializes once)
         static const hipError_t attr[2] = {

@@ -261,6 +261,7 @@ template <int TX, int SB, int XS, int RG, int SBQ, int KW>
 LuxStatus launch_k(const QmmArgs& a, hipStream_t st) {
     using L = Q4Lds<RG, XS, SBQ, KW>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
+    if (planned(a, "qgemv_q4_kernel")) return LuxStatus::Ok;
     if constexpr (L::kBytes > 64 * 1024) {
         // once per instantiation (a function-local static initializes once)
         static const hipError_t attr[2] = {

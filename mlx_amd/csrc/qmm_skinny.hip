@@ -10,6 +10,7 @@ LuxStatus launch_e(const QmmArgs& a, int KS, hipStream_t st) {
     const int tiles = kWaves / KS;
     const size_t lds = skinny_lds_bytes(a.M, a.K, a.K / GS, kSb, tiles);
     if (lds > 160 * 1024) return LuxStatus::NotSupported;
+    if (planned(a, "qmm_skinny_kernel")) return LuxStatus::Ok;
     auto kern = qmm_skinny_kernel<BITS, TX, SB, GS, GW, EPI>;
     // once per instantiation; a function-local static initializes exactly once
     // even when several threads make the first call together

@@ -163,6 +163,20 @@ class Context:
         return self.q.select_kernel(M, K, N, group_size, bits, x_dtype,
                                     x_dtype if sb_dtype is None else sb_dtype)
 
+    def kernel_name(self, M, K, N, group_size, bits, x_dtype, sb_dtype=None, out_dtype=None,
+                    kernel: int = abi.KERNEL_AUTO) -> Optional[str]:
+        """The gfx950 kernel op_quantized_matmul_ex launches for this shape
+        (lux_gpu_quantized_matmul_kernel_name: a dry run of the dispatch);
+        None where the op would fail.  sb/out dtypes default to x_dtype."""
+        f = getattr(self.be.handle, "lux_gpu_quantized_matmul_kernel_name", None)
+        if f is None:
+            return None
+        f.restype = ctypes.c_char_p
+        f.argtypes = [ctypes.c_int] * 9
+        sb = x_dtype if sb_dtype is None else sb_dtype
+        r = f(M, K, N, group_size, bits, x_dtype, sb, sb if out_dtype is None else out_dtype, kernel)
+        return None if r is None else r.decode()
+
     # base f32 tensor ops (vtable slots, as the reference core calls them)
     def binary_f32(self, op: str, a: Buffer, b: Buffer, out: Buffer, n: int) -> None:
         fn = getattr(self.vt, f"op_{op}_f32")

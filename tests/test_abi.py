@@ -75,7 +75,8 @@ def test_plugin_exports_exactly_the_declared_symbols():
     out = _run(["nm", "-D", "--defined-only", mlx_amd.PLUGIN_PATH])
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     declared = declared_symbols()
-    assert declared == {"lux_gpu_backend_init", "lux_gpu_backend_quant_init", "lux_gpu_quantized_matmul_noalloc"}
+    assert declared == {"lux_gpu_backend_init", "lux_gpu_backend_quant_init", "lux_gpu_quantized_matmul_noalloc",
+                        "lux_gpu_quantized_matmul_kernel_name"}
     assert declared <= exported
     # nothing else leaks from the plugin (hidden visibility)
     assert {s for s in exported if s.startswith("lux")} == declared
@@ -134,6 +135,81 @@ def test_quant_extension_table_without_gpu():
     assert q.op_quantized_matmul(None, None, None, None, None, None, 1, 64, 1, 64, 4, 1, 1, 1) == \
         abi.ERR_INVALID_ARGUMENT
     assert q.op_dequantize(None, None, None, None, None, 1, 64, 64, 4, 1, 1) == abi.ERR_INVALID_ARGUMENT
+
+
+def _kernel_name_fn():
+    import mlx_amd
+    lib = ctypes.CDLL(mlx_amd.PLUGIN_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    f = lib.lux_gpu_quantized_matmul_kernel_name
+    f.restype = ctypes.c_char_p
+    f.argtypes = [ctypes.c_int] * 9
+    return lambda *shape, kernel=0: (lambda r: None if r is None else r.decode())(f(*shape, kernel))
+
+
+@pytest.mark.skipif(bool(os.environ.get("LUX_HIP_GEMV_MAX_M") or os.environ.get("LUX_HIP_GEMM_RW")),
+                    reason="selection overridden by the environment")
+def test_auto_kernel_for_every_baseline_config():
+    """The kernel AUTO launches for each BASELINE configuration (a dry run of
+    the dispatch: host logic only), so a change of selection shows here."""
+    from mlx_amd import abi
+    name = _kernel_name_fn()
+    F32, F16, BF16 = abi.FLOAT32, abi.FLOAT16, abi.BFLOAT16
+    # (M, K, N, group, bits, x, scales/biases, out) -> kernel
+    configs = {
+        # c0: the CPU-backend GEMV case, all fp32
+        (1, 4096, 4096, 64, 4, F32, F32, F32): "qgemv_line_kernel",
+        # c1: decode, M = 1 / 4 / 8
+        (1, 4096, 14336, 64, 4, F16, F16, F16): "qgemv_line_kernel",
+        (4, 4096, 14336, 64, 4, F16, F16, F16): "qgemv_q4_kernel",
+        (8, 4096, 14336, 64, 4, F16, F16, F16): "qgemv_q4_kernel",
+        # c2: 8-bit, group 128, at the GEMV/GEMM crossover
+        (32, 8192, 8192, 128, 8, BF16, BF16, BF16): "qgemm_small_kernel",
+        # c3: prefill GEMM at both N
+        (2048, 4096, 4096, 64, 4, BF16, BF16, BF16): "qgemm_rw_kernel",
+        (2048, 4096, 14336, 64, 4, BF16, BF16, BF16): "qgemm_rw_kernel",
+        # c4: 3- and 6-bit codes at M = 1 and 64
+        (1, 4096, 11008, 64, 3, F16, F16, F16): "qgemv_line_kernel",
+        (1, 4096, 11008, 64, 6, F16, F16, F16): "qgemv_line_kernel",
+        (64, 4096, 11008, 64, 3, F16, F16, F16): "qgemm_small_kernel",
+        (64, 4096, 11008, 64, 6, F16, F16, F16): "qgemm_small_kernel",
+    }
+    for shape, want in configs.items():
+        assert name(*shape) == want, shape
+    # GEMV and GEMM choices of the same configs
+    assert name(1, 4096, 14336, 64, 4, F16, F16, F16, kernel=abi.KERNEL_GEMM) == "qgemm_kernel"
+    assert name(2048, 4096, 4096, 64, 4, BF16, BF16, BF16, kernel=abi.KERNEL_GEMV) == "qgemv_stream_kernel"
+    # errors and empty shapes
+    assert name(1, 100, 4096, 64, 4, F16, F16, F16) is None
+    assert name(2048, 4096, 4096, 64, 4, F32, F32, F32, kernel=abi.KERNEL_GEMM) is None
+    assert name(0, 4096, 4096, 64, 4, F16, F16, F16) == ""
+
+
+@pytest.mark.skipif(bool(os.environ.get("LUX_HIP_GEMV_MAX_M") or os.environ.get("LUX_HIP_GEMM_RW")),
+                    reason="selection overridden by the environment")
+def test_every_kernel_family_is_chosen_somewhere():
+    """Each kernel of the plugin is AUTO's choice for a class of shapes (none
+    is dead code); one representative shape per kernel."""
+    from mlx_amd import abi
+    name = _kernel_name_fn()
+    F32, F16, BF16 = abi.FLOAT32, abi.FLOAT16, abi.BFLOAT16
+    families = {
+        "qgemv_line_kernel": (1, 4096, 14336, 64, 4, F16),       # M = 1, K up to 16384
+        "qgemv_split_kernel": (1, 14336, 4096, 64, 4, F16),      # M = 1 down projections, K > 8192
+        "qgemv_stream_kernel": (2, 4096, 14336, 64, 3, F16),     # M = 2..8, 3/5/6-bit codes
+        "qgemv_kernel": (4, 4096, 11008, 64, 3, F32),            # f32 x, 3/5/6-bit codes, M >= 2
+        "qgemv_mx_kernel": (4, 4096, 14336, 64, 8, F16),         # M = 2..4, 8-bit codes
+        "qgemv_q4_kernel": (4, 4096, 14336, 64, 4, F16),         # M = 2..8, 4-bit codes, K = 4096
+        "qgemv_dec_kernel": (6, 8192, 8192, 64, 4, F16),         # M = 5..8, 4-bit codes, K = 8192
+        "qgemv_mid_kernel": (12, 4096, 14336, 64, 4, F16),       # M = 9..16, 4/8-bit codes
+        "qmm_skinny_kernel": (6, 4096, 14336, 64, 8, F16),       # M = 5..8, 8-bit codes, K <= 4096
+        "qgemm_small_kernel": (32, 8192, 8192, 128, 8, BF16),    # 8 < M <= 64
+        "qgemm_sk_kernel": (32, 4096, 28672, 64, 4, BF16),       # 8 < M <= 64, wide N
+        "qgemm_rw_kernel": (2048, 4096, 4096, 64, 4, BF16),      # M > 64, 4/8-bit, K % 1024 == 0
+        "qgemm_kernel": (2048, 4096, 11008, 64, 3, BF16),        # M > 64, other widths or K
+        "qmm_generic_kernel": (1, 96, 256, 32, 4, F16),          # K % 64 != 0
+    }
+    for want, (M, K, N, gs, bits, xd) in families.items():
+        assert name(M, K, N, gs, bits, xd, xd, xd) == want, (want, M, K, N, gs, bits, xd)
 
 
 # ------------------------------------------------------------- loader ------
