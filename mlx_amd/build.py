@@ -37,6 +37,9 @@ CFLAGS = [
     "-Wall",
     # packed fp32 VALU ops are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # device code objects stored compressed in the library (the HIP runtime
+    # expands them when it loads the module): about a quarter of the size
+    "--offload-compress",
 ]
 
 

@@ -37,18 +37,39 @@ def _tool(name):
 
 @pytest.fixture(scope="module")
 def code_objects(tmp_path_factory):
-    """The plugin's embedded gfx950 code objects, unpacked into a temp dir."""
+    """The plugin's embedded gfx950 code objects, unpacked into a temp dir.
+
+    The plugin stores them as compressed offload bundles ("CCOB" header:
+    magic, u16 version, u16 method, then the bundle's total size, u64 in
+    version 3, u32 before) in its .hip_fatbin section; each bundle is cut
+    out at its stated size and unbundled by clang-offload-bundler."""
+    import struct
+
     import mlx_amd
-    objdump = _tool("llvm-objdump")
-    if not objdump:
-        pytest.skip("llvm-objdump not available")
+    objdump, objcopy, bundler = _tool("llvm-objdump"), _tool("llvm-objcopy"), _tool("clang-offload-bundler")
+    if not (objdump and objcopy and bundler):
+        pytest.skip("llvm-objdump / llvm-objcopy / clang-offload-bundler not available")
     assert os.path.exists(mlx_amd.PLUGIN_PATH), "run __graft_entry__.build() first"
     d = tmp_path_factory.mktemp("codeobj")
-    so = d / "plugin.so"
-    shutil.copy(mlx_amd.PLUGIN_PATH, so)
-    # --offloading writes the embedded device code objects next to its input
-    subprocess.run([objdump, "--offloading", str(so)], cwd=d, check=True, capture_output=True)
-    cos = sorted(d.glob("plugin.so.*gfx950*"))
+    fat = d / "fatbin.bin"
+    subprocess.run([objcopy, "-O", "binary", "--only-section=.hip_fatbin", mlx_amd.PLUGIN_PATH, str(fat)],
+                   check=True, capture_output=True)
+    data = fat.read_bytes()
+    cos, i = [], data.find(b"CCOB")
+    while i >= 0:
+        ver = struct.unpack_from("<H", data, i + 4)[0]
+        size = struct.unpack_from("<Q" if ver >= 3 else "<I", data, i + 8)[0]
+        src, out = d / f"b{len(cos)}.ccob", d / f"b{len(cos)}.gfx950.co"
+        src.write_bytes(data[i:i + size])
+        subprocess.run([bundler, "--unbundle", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                        f"--input={src}", f"--output={out}"], check=True, capture_output=True)
+        cos.append(out)
+        i = data.find(b"CCOB", i + size)
+    if not cos:  # uncompressed bundles: --offloading writes them next to its input
+        so = d / "plugin.so"
+        shutil.copy(mlx_amd.PLUGIN_PATH, so)
+        subprocess.run([objdump, "--offloading", str(so)], cwd=d, check=True, capture_output=True)
+        cos = sorted(d.glob("plugin.so.*gfx950*"))
     assert cos, "no gfx950 code object in the plugin"
     return cos
 
