@@ -270,6 +270,8 @@ def ceiling_lib():
     L = ctypes.CDLL(path)
     L.lux_ceiling_empty.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     L.lux_ceiling_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    L.lux_ceiling_empty_loop.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.POINTER(ctypes.c_float)]
     return L
 
 
@@ -300,6 +302,12 @@ def ceiling_leg(ctx, hip, nbytes, steps, warmup, blocks):
             if name == "read":
                 out[name]["frac_of_peak"] = round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
                 out[name]["graph_frac_of_peak"] = round(nbytes / g / 1e6 / HBM_PEAK_GBS, 4)
+        # the same empty launches issued from a C loop (no Python call per
+        # launch), after the leg's own warm-up
+        ms = ctypes.c_float()
+        hip.ck(L.lux_ceiling_empty_loop(steps, blocks, sink, ctypes.c_void_p(stream), ctypes.byref(ms)),
+               "lux_ceiling_empty_loop")
+        out["empty"]["c_loop_us_per_launch"] = round(ms.value * 1e3 / steps, 3)
         out["bytes"] = nbytes
         out["empty_blocks"] = blocks
     finally:

@@ -69,4 +69,28 @@ __attribute__((visibility("default"))) int lux_ceiling_read(const void* buf, uin
     return (int)hipGetLastError();
 }
 
+// `n` launches of the empty kernel (`blocks` blocks) issued back to back
+// from this C loop, between two events on `stream`: the per-launch floor
+// without a Python call per launch.  *ms_out: the events' elapsed time.
+// Returns the first hipError_t met.
+__attribute__((visibility("default"))) int lux_ceiling_empty_loop(int n, int blocks, void* sink, void* stream,
+                                                                  float* ms_out) {
+    if (n <= 0 || blocks <= 0 || ms_out == nullptr) return (int)hipErrorInvalidValue;
+    const hipStream_t st = (hipStream_t)stream;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipEventRecord(e0, st);
+    for (int i = 0; i < n && e == hipSuccess; i++) {
+        hipLaunchKernelGGL(ceiling_empty_kernel, dim3(blocks), dim3(kThreads), 0, st, static_cast<uint32_t*>(sink), 0);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms_out, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    return (int)e;
+}
+
 }  // extern "C"
