@@ -192,14 +192,42 @@ def calibrate_copy(hip, nbytes, reps=8):
     print(json.dumps({"calibrate_copy_bytes": nbytes, "reps": reps}), flush=True)
 
 
-def make_weights(ctx, N, K, bits, gs, sb, copies, seed):
-    """W ~ N(0, 0.02) on the host, quantized on the GPU by the plugin's
-    op_quantize into `copies` distinct buffer sets."""
+# ---- synthetic inputs: the fixtures' portable generator -------------------
+# x ~ N(0, 1) from stream 4 seed + 1, W ~ N(0, 0.02) from stream 4 seed + 2
+# and, for configs[4], 1 % of W's entries scaled by 20 (chosen by a stable
+# sort of the u32 stream 4 seed + 3): the tensors whose SHA-256 digests
+# tests/golden/digests.json holds (each leg's copy-0 weights are checked
+# against them; digest_match in the line).
+DIGESTS = os.path.join(ROOT, "tests", "golden", "digests.json")
+_W_CACHE = {}
+
+
+def rng_normal(n, seed, std=1.0):
+    L = ceiling_lib()
+    out = np.empty(n, dtype=np.float32)
+    L.lux_bench_rng_normal_f32(out.ctypes.data, n, seed, 0.0, std)
+    return out
+
+
+def w_host(N, K, seed, outliers):
+    key = (N, K, seed, outliers)
+    if key not in _W_CACHE:
+        _W_CACHE.clear()
+        w = rng_normal(N * K, seed * 4 + 2, 0.02)
+        if outliers:
+            L = ceiling_lib()
+            u = np.empty(N * K, dtype=np.uint32)
+            L.lux_bench_rng_u32(u.ctypes.data, N * K, seed * 4 + 3)
+            w[u.argsort(kind="stable")[:int(round(0.01 * N * K))]] *= np.float32(20.0)
+        _W_CACHE[key] = w.reshape(N, K)
+    return _W_CACHE[key]
+
+
+def make_weights(ctx, N, K, bits, gs, sb, copies, seed, outliers=False):
+    """W on the host (the generator above), quantized on the GPU by the
+    plugin's op_quantize into `copies` distinct buffer sets."""
     from mlx_amd import runtime
-    rng = np.random.default_rng(seed)
-    w = (rng.standard_normal(N * K, dtype=np.float32) * np.float32(0.02)).reshape(N, K)
-    wb = ctx.upload(w)
-    del w
+    wb = ctx.upload(w_host(N, K, seed, outliers))
     G = K // gs
     sets = []
     for _ in range(copies):
@@ -213,13 +241,30 @@ def make_weights(ctx, N, K, bits, gs, sb, copies, seed):
     return sets
 
 
+def digest_match(K, N, bits, gs, sb, seed, outliers, w_q, s, b):
+    """Whether copy 0's quantized weights hash to the committed digests of
+    the config with this shape (None where no digest covers it)."""
+    import hashlib
+    try:
+        with open(DIGESTS) as f:
+            table = json.load(f)
+    except OSError:
+        return None
+    for d in table.values():
+        if (d["shape"][1:] == [K, N] and d["bits"] == bits and d["group_size"] == gs and d["sb_dtype"] == sb
+                and d["seed"] == seed and bool(d.get("outlier_frac")) == outliers):
+            got = {n: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+                   for n, a in (("w_q", w_q), ("scales", s), ("biases", b))}
+            return all(got[n] == d["sha256"][n] for n in got)
+    return None
+
+
 def weight_bytes(N, K, bits, gs, sb):
     return N * K * bits // 8 + 2 * N * (K // gs) * (4 if sb == F32 else 2)
 
 
 def x_host(M, K, xd, seed):
-    rng = np.random.default_rng(seed + 7)
-    x32 = rng.standard_normal(M * K, dtype=np.float32).reshape(M, K)
+    x32 = rng_normal(M * K, seed * 4 + 1).reshape(M, K)
     if xd == F16:
         return x32.astype(np.float16).view(np.uint16)
     if xd == BF16:
@@ -229,13 +274,19 @@ def x_host(M, K, xd, seed):
 
 
 def bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, kernel, copies=COPIES, seed=1,
-              keep=False):
+              keep=False, outliers=False):
     """Times `steps` launches over `copies` rotating weight sets; keep=True
-    also returns copy 0's inputs and output (downloaded) for the parity check."""
+    also returns copy 0's inputs and output (downloaded) for the parity check.
+    r["digest_match"]: copy 0's weights against the committed digests."""
     from mlx_amd import runtime
     xh = x_host(M, K, xd, seed)
     xb = ctx.upload(xh)
-    sets = make_weights(ctx, N, K, bits, gs, sbd, copies, seed)
+    sets = make_weights(ctx, N, K, bits, gs, sbd, copies, seed, outliers)
+    sbnp = runtime.np_dtype(sbd)
+    wq0, s0, b0 = sets[0]
+    wq0h = wq0.download(np.uint32, (N, K * bits // 32))
+    s0h, b0h = s0.download(sbnp, (N, K // gs)), b0.download(sbnp, (N, K // gs))
+    dm = digest_match(K, N, bits, gs, sbd, seed, outliers, wq0h, s0h, b0h)
     out = ctx.alloc(M * N * runtime.esize(od))
     stream = ctx.stream
 
@@ -246,16 +297,13 @@ def bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, kernel, c
     r = time_launches(hip, stream, step, steps, max(warmup, copies))
     r["graph_ms_per_launch"] = time_graph(hip, stream, step)
     r["steps"] = steps
+    r["digest_match"] = dm
     if keep:
         step(0)
         ctx.sync()
         r["y"] = out.download(runtime.np_dtype(od), (M, N))
         r["x"] = xh
-        wq, s, b = sets[0]
-        sbnp = runtime.np_dtype(sbd)
-        r["w_q"] = wq.download(np.uint32, (N, K * bits // 32))
-        r["s"] = s.download(sbnp, (N, K // gs))
-        r["b"] = b.download(sbnp, (N, K // gs))
+        r["w_q"], r["s"], r["b"] = wq0h, s0h, b0h
     for t in [xb, out] + [b for st in sets for b in st]:
         t.free()
     return r
@@ -272,6 +320,9 @@ def ceiling_lib():
     L.lux_ceiling_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
     L.lux_ceiling_empty_loop.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.POINTER(ctypes.c_float)]
+    L.lux_bench_rng_normal_f32.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
+                                           ctypes.c_float]
+    L.lux_bench_rng_u32.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64]
     return L
 
 
@@ -492,7 +543,7 @@ def config_legs(ctx, hip, steps, warmup, keep=False):
     for name, M, K, N, bits, gs, xd, sbd, od in CONFIG_LEGS:
         wb = weight_bytes(N, K, bits, gs, sbd)
         r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, abi.KERNEL_AUTO,
-                      copies=copies_for(wb), keep=keep and name == "c2")
+                      copies=copies_for(wb), keep=keep and name == "c2", outliers=name == "c4")
         t = r["event_ms_per_launch"] * 1e-3
         flops = 2.0 * M * N * K
         key = f"{name}_m{M}_{bits}bit"
@@ -503,7 +554,7 @@ def config_legs(ctx, hip, steps, warmup, keep=False):
                     "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
                     "tflops": round(flops / t / 1e12, 2),
                     "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4),
-                    "copies": copies_for(wb)}
+                    "copies": copies_for(wb), "digest_match": r["digest_match"]}
         if keep and name == "c2":
             runs["c2"] = r
     return out, runs
@@ -517,7 +568,8 @@ def sweep(ctx, hip, steps, only=None, table=SWEEP):
         if only and name not in only:
             continue
         copies = 4 if M >= 256 else copies_for(weight_bytes(N, K, bits, gs, sbd))
-        r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, 8, abi.KERNEL_AUTO, copies=copies)
+        r = bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, 8, abi.KERNEL_AUTO, copies=copies,
+                      outliers=name == "c4")
         t = r["event_ms_per_launch"] * 1e-3
         wb = weight_bytes(N, K, bits, gs, sbd)
         flops = 2.0 * M * N * K
@@ -527,7 +579,8 @@ def sweep(ctx, hip, steps, only=None, table=SWEEP):
                           "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
                           "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
                           "tflops": round(flops / t / 1e12, 2),
-                          "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4)}), flush=True)
+                          "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4),
+                          "digest_match": r["digest_match"]}), flush=True)
 
 
 def decode_legs(ctx, hip, K, N, bits, gs, steps, warmup):
@@ -541,7 +594,8 @@ def decode_legs(ctx, hip, K, N, bits, gs, steps, warmup):
         out[f"M{m}"] = {"kernel": ctx.kernel_name(m, K, N, gs, bits, F16, F16, F16),
                         "kernel_us_avg": round(t * 1e6, 3), "kernel_us_median": r["per_launch_us"]["median"],
                         "graph_us": round(r["graph_ms_per_launch"] * 1e3, 3),
-                        "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4)}
+                        "weight_GBs": round(wb / t / 1e9, 1), "hbm_frac": round(wb / t / 1e9 / HBM_PEAK_GBS, 4),
+                        "digest_match": r["digest_match"]}
     return out
 
 
@@ -631,7 +685,8 @@ def main():
                              "kernel_us_median": rg["per_launch_us"]["median"],
                              "per_launch_us": rg["per_launch_us"],
                              "graph_us": round(rg["graph_ms_per_launch"] * 1e3, 2),
-                             "wall_tflops": round(flops * rg["steps"] / rg["wall_s"] / 1e12, 2)}
+                             "wall_tflops": round(flops * rg["steps"] / rg["wall_s"] / 1e12, 2),
+                             "digest_match": rg["digest_match"]}
             runs[n] = rg
         return gemm, runs
 
@@ -657,8 +712,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic: x~N(0,1) f16; W~N(0,0.02) quantized on the GPU (4-bit, group 64, "
-                "f16 scales/biases); 16 rotated weight copies",
+        "data": "synthetic, seed 1, from the test fixtures' portable generator (xoshiro256** + Box-Muller): "
+                "x~N(0,1) f16, W~N(0,0.02) quantized on the GPU (4-bit, group 64, f16 scales/biases); "
+                "16 rotated weight copies; copy 0 hashes to the committed digests: " + str(r["digest_match"]),
         "config": {"workload": "configs[1] decode GEMV M=1", "M": M, "K": K, "N": N, "bits": bits,
                    "group_size": gs, "kernel": ctx.kernel_name(M, K, N, gs, bits, F16, F16, F16),
                    "hbm_pct": round(100 * value / HBM_PEAK_GBS, 2)},

@@ -1,4 +1,5 @@
-// ceiling.hip -- measurement kernels for bench.py's ceiling leg (gfx950).
+// ceiling.hip -- measurement kernels for bench.py's ceiling leg (gfx950),
+// and the seeded generator of bench.py's synthetic inputs.
 //
 // Built into its own library (libluxgpu_ceiling.so), not into the plugin.
 // They bound what any single launch of the decode GEMV can show on this
@@ -11,6 +12,7 @@
 //     read pattern measured for 33 MB; the words are folded and stored only
 //     if they equal a value random data does not produce, so the loads stay.
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 namespace {
@@ -91,6 +93,60 @@ __attribute__((visibility("default"))) int lux_ceiling_empty_loop(int n, int blo
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     return (int)e;
+}
+
+}  // extern "C"
+
+// ---- synthetic inputs ------------------------------------------------------
+// The portable generator the test fixtures are made with (their SHA-256
+// digests are committed), so that bench.py times the same tensors:
+// xoshiro256** seeded through splitmix64; normals by Box-Muller on 53-bit
+// uniforms u1 in (0, 1], u2 in [0, 1), two per pair of draws.
+
+namespace {
+uint64_t splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+struct Xoshiro {
+    uint64_t s[4];
+    explicit Xoshiro(uint64_t seed) {
+        uint64_t sm = seed;
+        for (int i = 0; i < 4; i++) s[i] = splitmix64(&sm);
+    }
+    static uint64_t rotl(uint64_t v, int k) { return (v << k) | (v >> (64 - k)); }
+    uint64_t next() {
+        const uint64_t r = rotl(s[1] * 5, 7) * 9, t = s[1] << 17;
+        s[2] ^= s[0]; s[3] ^= s[1]; s[1] ^= s[2]; s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = rotl(s[3], 45);
+        return r;
+    }
+};
+}  // namespace
+
+extern "C" {
+
+// n normals of mean `mean` and deviation `stddev` into out (host memory)
+__attribute__((visibility("default"))) void lux_bench_rng_normal_f32(float* out, size_t n, uint64_t seed, float mean,
+                                                                     float stddev) {
+    Xoshiro x(seed);
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        const double u1 = (double)((x.next() >> 11) + 1) * 0x1.0p-53;
+        const double u2 = (double)(x.next() >> 11) * 0x1.0p-53;
+        const double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(mean + stddev * (r * cos(two_pi * u2)));
+        if (i + 1 < n) out[i + 1] = (float)(mean + stddev * (r * sin(two_pi * u2)));
+    }
+}
+
+// n uniform 32-bit words (the high halves of the draws) into out
+__attribute__((visibility("default"))) void lux_bench_rng_u32(uint32_t* out, size_t n, uint64_t seed) {
+    Xoshiro x(seed);
+    for (size_t i = 0; i < n; i++) out[i] = (uint32_t)(x.next() >> 32);
 }
 
 }  // extern "C"

@@ -44,13 +44,15 @@ CASES = [
 ]
 
 # full-size synthetic inputs of the configs, seed 1
+# (name, M, K, N, bits, group, x dtype, scale dtype, fraction of W entries
+# scaled x20: configs[4]'s outliers)
 DIGEST_CASES = [
-    ("c0", 1, 4096, 4096, 4, 64, F32, F32),
-    ("c1", 8, 4096, 14336, 4, 64, F16, F16),
-    ("c2", 32, 8192, 8192, 8, 128, BF16, BF16),
-    ("c3_n4096", 2048, 4096, 4096, 4, 64, BF16, BF16),
-    ("c4_b3", 64, 4096, 11008, 3, 64, F16, F16),
-    ("c4_b6", 64, 4096, 11008, 6, 64, F16, F16),
+    ("c0", 1, 4096, 4096, 4, 64, F32, F32, 0.0),
+    ("c1", 8, 4096, 14336, 4, 64, F16, F16, 0.0),
+    ("c2", 32, 8192, 8192, 8, 128, BF16, BF16, 0.0),
+    ("c3_n4096", 2048, 4096, 4096, 4, 64, BF16, BF16, 0.0),
+    ("c4_b3", 64, 4096, 11008, 3, 64, F16, F16, 0.01),
+    ("c4_b6", 64, 4096, 11008, 6, 64, F16, F16, 0.01),
 ]
 
 
@@ -82,25 +84,26 @@ def build_case(key, M, K, N, bits, gs, xd, sbd, special):
             "meta": np.array([M, K, N, bits, gs, xd, sbd], np.int32)}
 
 
-def digest_case(M, K, N, bits, gs, xd, sbd):
+def digest_case(M, K, N, bits, gs, xd, sbd, outlier_frac=0.0):
     from oracle import oracle as O
-    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=1)
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=1, outlier_frac=outlier_frac)
     return {name: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
             for name, a in (("x", x), ("w_q", w_q), ("scales", s), ("biases", b))}
 
 
-def main():
+def main(digests_only=False):
     from oracle import oracle as O
     if not os.path.exists(O.LIB_PATH):
         O.build()
-    arrays = {}
-    for key, *c in CASES:
-        for name, a in build_case(key, *c).items():
-            arrays[f"{key}/{name}"] = a
-    np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)
+    if not digests_only:
+        arrays = {}
+        for key, *c in CASES:
+            for name, a in build_case(key, *c).items():
+                arrays[f"{key}/{name}"] = a
+        np.savez_compressed(os.path.join(HERE, "golden.npz"), **arrays)
     digests = {name: {"shape": [M, K, N], "bits": bits, "group_size": gs, "x_dtype": xd, "sb_dtype": sbd,
-                      "seed": 1, "sha256": digest_case(M, K, N, bits, gs, xd, sbd)}
-               for name, M, K, N, bits, gs, xd, sbd in DIGEST_CASES}
+                      "seed": 1, "outlier_frac": of, "sha256": digest_case(M, K, N, bits, gs, xd, sbd, of)}
+               for name, M, K, N, bits, gs, xd, sbd, of in DIGEST_CASES}
     with open(os.path.join(HERE, "digests.json"), "w") as f:
         json.dump(digests, f, indent=1, sort_keys=True)
         f.write("\n")
@@ -108,4 +111,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(digests_only="--digests-only" in sys.argv)

@@ -101,5 +101,6 @@ def test_full_size_digests(oracle):
     from make_fixtures import DIGEST_CASES, digest_case
     with open(os.path.join(GOLD, "digests.json")) as f:
         want = json.load(f)
-    for name, M, K, N, bits, gs, xd, sbd in DIGEST_CASES:
-        assert digest_case(M, K, N, bits, gs, xd, sbd) == want[name]["sha256"], name
+    for name, M, K, N, bits, gs, xd, sbd, outlier_frac in DIGEST_CASES:
+        assert want[name]["outlier_frac"] == outlier_frac, name
+        assert digest_case(M, K, N, bits, gs, xd, sbd, outlier_frac) == want[name]["sha256"], name
