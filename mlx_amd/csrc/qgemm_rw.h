@@ -43,11 +43,16 @@
 // product is exactly s q: each value is fmaf(s, q, b) bit for bit, one
 // instruction per code (2^(24-p) s is exact for |s| < 2^103).
 //
-// Grid: one block per tile (K halves for a split last round, qsplit.h); the
-// output tile is staged in LDS and stored as whole 16-byte chunks of rows.
-// Tiles are dealt to the 8 XCDs (block b runs on XCD b % 8) in 4 x 8 groups
-// of M x N tiles, so the 32 blocks an XCD runs at once share 4 x slabs and
-// 8 W slabs in its L2.
+// Work units: tiles (K halves for a split last round, K parts for a shape
+// with few tiles; qsplit.h).  Grid: one block per unit, or, where there are
+// more units than CUs and the output is 16-bit, one block per CU running
+// units b, b + 256, ... (whole tiles first, halves last): at each hand-over
+// the next unit's first transfers go out before the finished tile is
+// staged and stored, so its prologue latency runs under the output stage,
+// and no block waits for a slot.  The output tile is staged in LDS and
+// stored as whole 16-byte chunks of rows.  Tiles are dealt to the 8 XCDs
+// (block b runs on XCD b % 8) in 4 x 8 groups of M x N tiles, so the 32
+// blocks an XCD runs at once share 4 x slabs and 8 W slabs in its L2.
 #pragma once
 #include <cstdlib>
 
@@ -471,23 +476,14 @@ __device__ __forceinline__ Unit unit_of(int u, int tiles, int split_from, int ns
     return w;
 }
 
-// Grid: one block per unit; block b runs unit b.
-template <class C, bool EPI>
-__global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep, int mtiles,
-    int ntiles, int split_from, int nsplit, void* __restrict__ ws, uint32_t epoch) {
-    constexpr int NT = C::NT, BITS = C::BITS, NW = C::NW, GS = C::GS, MT = C::MT, BM = C::BM;
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+// the K-loop constants of unit w for this wave and lane
+template <class C>
+__device__ __forceinline__ void setup_ctx(Ctx<C>& t, const Unit& w, uint8_t* lds, const uint16_t* x,
+                                          const uint32_t* wq, const void* scales, const void* biases, int M, int K,
+                                          int N, int wave, int lane) {
+    constexpr int NT = C::NT, BITS = C::BITS, NW = C::NW, GS = C::GS, BM = C::BM;
     const int c = lane & 31, h = lane >> 5;
-    const int tiles = mtiles * ntiles;
-
-    const Unit w = unit_of<C>(blockIdx.x, tiles, split_from, nsplit, mtiles, ntiles, K / BK);
     const int m0 = w.m0, n0 = w.n0, k0 = w.k0;
-
-    Ctx<C> t;
     t.lds = lds;
     t.lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     t.x = reinterpret_cast<const uint8_t*>(x) + (size_t)k0 * BK * 2;
@@ -531,46 +527,183 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     t.sw = swz(c);
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) t.sb_lds[tt] = wave * C::WN * 32 + (32 * tt + c) * 16;
+}
 
-    f32x16 acc[MT][NT];
+// rows [32 I0, 32 I1) of the block's tile, through the output stage, in
+// 16-bit type TO into LDS at dst (row stride rs bytes, row 32 I0 first):
+// lane (c, h) holds column c and rows 8 (v / 4) + 4 h + v % 4 of each 32 x
+// 32 tile, so VGPRs v and v + 1 are two rows of one column, converted
+// together
+template <class C, bool EPI, int TO, int I0 = 0, int I1 = C::MT>
+__device__ __forceinline__ void stage16(uint8_t* dst, int rs, const f32x16 (&acc)[C::MT][C::NT], const Epilogue& ep,
+                                        int n0, int N, int wave, int c, int h) {
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int i = I0; i < I1; i++)
 #pragma unroll
-        for (int tt = 0; tt < NT; tt++)
+        for (int tt = 0; tt < C::NT; tt++) {
+            const int nl = wave * C::WN + 32 * tt + c;  // column within the tile
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][tt][v] = 0.f;
+            for (int v = 0; v < 16; v += 2) {
+                const int ml = 32 * (i - I0) + 8 * (v >> 2) + 4 * h + (v & 3);
+                float o0 = acc[i][tt][v], o1 = acc[i][tt][v + 1];
+                if constexpr (EPI) {
+                    if (n0 + nl < N) {
+                        o0 = apply_epilogue(ep, (size_t)(n0 + nl), o0);
+                        o1 = apply_epilogue(ep, (size_t)(n0 + nl), o1);
+                    }
+                }
+                const uint32_t pk = pack2<TO>(o0, o1);
+                uint8_t* d = dst + ml * rs + nl * 2;
+                *reinterpret_cast<uint16_t*>(d) = (uint16_t)pk;
+                *reinterpret_cast<uint16_t*>(d + rs) = (uint16_t)(pk >> 16);
+            }
+        }
+}
 
-    // prologue: the batches of steps 0 .. D - 1, then wait for those of
-    // steps 0 .. BAR - 1; the "previous sub-step 3" of step 0 is zeros (its
-    // MFMAs add +0 to the +0 accumulators)
-    Regs<C> r;
-#pragma unroll
-    for (int i = 0; i < MT; i++) r.a3[i] = u4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int tt = 0; tt < NT; tt++) r.b3[tt] = u4{0u, 0u, 0u, 0u};
-    prologue_issue<C, 0>(t);
-    {
-        constexpr int n = [] {
-            int v = 0;
-            for (int d = C::BAR; d < C::D; d++) v += C::batch(d);
-            return v;
-        }();
-        wait_vm<n>();
-    }
+// a 16-bit output tile handed over in a persistent grid: 16-byte chunks per
+// thread (chunk j of thread tid: row tid / 32 + 16 j, columns 8 (tid % 32)
+// ..+8), and the LDS above the rings where it is staged half its rows at a
+// time while the next unit's first transfers land -- where that fits; else
+// it is staged in the rings before those transfers are issued
+template <class C>
+constexpr int kHand = C::BM * BN * 2 / 16 / C::kThreads;
+template <class C>
+constexpr int kHandLds = C::BM / 2 * (BN * 2 + 16);
+template <class C>
+constexpr bool kStageAbove = C::kLds + kHandLds<C> <= 160 * 1024;
+
+// half P of a handed-over tile (rows P BM / 2 ..+BM / 2) staged at hs and
+// read back as the thread's chunks P kHand / 2 ..
+template <class C, bool EPI, int P>
+__device__ __forceinline__ void hand_half(uint8_t* hs, int rs, const f32x16 (&acc)[C::MT][C::NT], const Epilogue& ep,
+                                          int n0, int N, int wave, int c, int h, int tid, u4 (&val)[kHand<C>]) {
+    constexpr int I0 = P * C::MT / 2, I1 = I0 + C::MT / 2, kHalf = kHand<C> / 2;
+    if (ep.out_dt == DT_BF16) stage16<C, EPI, DT_BF16, I0, I1>(hs, rs, acc, ep, n0, N, wave, c, h);
+    else stage16<C, EPI, DT_F16, I0, I1>(hs, rs, acc, ep, n0, N, wave, c, h);
     barrier();
-    {
-        uint32_t rs[NT], rb[NT];
-        read_step(t, 0, r.cw, rs, rb);
-        factors<C::SB, NT>(rs, rb, r.f);
+#pragma unroll
+    for (int i = 0; i < kHalf; i++) {
+        const int q = tid + i * C::kThreads;
+        val[P * kHalf + i] = *reinterpret_cast<const u4*>(hs + (q >> 5) * rs + (q & 31) * 16);
     }
-    read_a(t, 0, 0, r.a);
+}
 
-    // KT is a multiple of kUnroll (the launcher's split rules keep it so)
-    for (int kt = 0; kt < w.KT; kt += C::kUnroll) steps<C, 0>(t, r, acc, kt);
-    // sub-step 3 of the last step
-    mfmas<C::TX, MT, NT>(acc, r.a3, r.b3);
-    // no transfer may still be landing when LDS is next written
-    wait_vm<0>();
+// Grid: one block per unit (block b runs unit b), or fewer blocks than
+// units: block b runs units b, b + grid, ... -- the launcher does so only
+// for 16-bit outputs in 16-byte chunks (N % 8 == 0, y aligned) with 31-bit
+// offsets, and with whole tiles before the halves (a half is always the
+// last unit of its block)
+template <class C, bool EPI>
+__global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
+    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, Epilogue ep, int mtiles,
+    int ntiles, int split_from, int nsplit, void* __restrict__ ws, uint32_t epoch, int units) {
+    constexpr int NT = C::NT, MT = C::MT, BM = C::BM;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, h = lane >> 5;
+    const int tiles = mtiles * ntiles;
+
+    int u = blockIdx.x;
+    Unit w = unit_of<C>(u, tiles, split_from, nsplit, mtiles, ntiles, K / BK);
+    Ctx<C> t;
+    setup_ctx<C>(t, w, lds, x, wq, scales, biases, M, K, N, wave, lane);
+    // the next unit's context and its first D steps' transfers
+    auto next_unit = [&](int un) {
+        u = un;
+        w = unit_of<C>(u, tiles, split_from, nsplit, mtiles, ntiles, K / BK);
+        setup_ctx<C>(t, w, lds, x, wq, scales, biases, M, K, N, wave, lane);
+        prologue_issue<C, 0>(t);
+    };
+    prologue_issue<C, 0>(t);
+    f32x16 acc[MT][NT];
+    bool handed = false;  // the previous unit's output stores follow this unit's first transfers
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[i][tt][v] = 0.f;
+
+        // prologue: the batches of steps 0 .. D - 1 are in flight; wait for
+        // those of steps 0 .. BAR - 1 (vmcnt counts in issue order: the
+        // younger batches and a handed-over tile's stores may still be in
+        // flight).  The "previous sub-step 3" of step 0 is zeros (its MFMAs
+        // add +0 to the +0 accumulators)
+        Regs<C> r;
+#pragma unroll
+        for (int i = 0; i < MT; i++) r.a3[i] = u4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int tt = 0; tt < NT; tt++) r.b3[tt] = u4{0u, 0u, 0u, 0u};
+        {
+            constexpr int n = [] {
+                int v = 0;
+                for (int d = C::BAR; d < C::D; d++) v += C::batch(d);
+                return v;
+            }();
+            if (handed) wait_vm<n + kHand<C>>();
+            else wait_vm<n>();
+        }
+        barrier();
+        {
+            uint32_t rs[NT], rb[NT];
+            read_step(t, 0, r.cw, rs, rb);
+            factors<C::SB, NT>(rs, rb, r.f);
+        }
+        read_a(t, 0, 0, r.a);
+
+        // KT is a multiple of kUnroll (the launcher's split rules keep it so)
+        for (int kt = 0; kt < w.KT; kt += C::kUnroll) steps<C, 0>(t, r, acc, kt);
+        // sub-step 3 of the last step
+        mfmas<C::TX, MT, NT>(acc, r.a3, r.b3);
+        // no transfer may still be landing when LDS is next written
+        wait_vm<0>();
+        const int un = u + (int)gridDim.x;
+        if (un >= units || w.part >= 0) break;
+
+        // ---- hand-over to unit un: every wave is past its K loop (the
+        // rings are free after this barrier) ----
+        barrier();
+        const int mo = w.m0, no = w.n0;
+        constexpr int rs = BN * 2 + 16;  // staging row stride: rows m and m + 4 in different banks
+        u4 val[kHand<C>];
+        if constexpr (kStageAbove<C>) {
+            // the next unit's transfers first, then the tile above the
+            // rings in two passes of BM / 2 rows
+            next_unit(un);
+            uint8_t* hs = lds + C::kLds;
+            hand_half<C, EPI, 0>(hs, rs, acc, ep, no, N, wave, c, h, tid, val);
+            barrier();
+            hand_half<C, EPI, 1>(hs, rs, acc, ep, no, N, wave, c, h, tid, val);
+        } else {
+            // the tile in the rings in one pass, then the next unit's transfers
+            if (ep.out_dt == DT_BF16) stage16<C, EPI, DT_BF16>(lds, rs, acc, ep, no, N, wave, c, h);
+            else stage16<C, EPI, DT_F16>(lds, rs, acc, ep, no, N, wave, c, h);
+            barrier();
+#pragma unroll
+            for (int i = 0; i < kHand<C>; i++) {
+                const int q = tid + i * C::kThreads;
+                val[i] = *reinterpret_cast<const u4*>(lds + (q >> 5) * rs + (q & 31) * 16);
+            }
+            barrier();
+            next_unit(un);
+        }
+        // the stores: chunks past M or N (whole chunks, N % 8 == 0) get an
+        // offset past the buffer's end, which the hardware drops, so every
+        // thread issues exactly kHand stores after the next unit's transfers
+        const __amdgpu_buffer_rsrc_t yr =
+            __builtin_amdgcn_make_buffer_rsrc(y, 0, (int)((uint32_t)M * (uint32_t)N * 2u), 0x00020000);
+#pragma unroll
+        for (int j = 0; j < kHand<C>; j++) {
+            const int m = mo + (tid >> 5) + 16 * j, n = no + (tid & 31) * 8;
+            const uint32_t off = m < M && n < N ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * 2u : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b128(val[j], yr, off, 0, 0);
+        }
+        handed = true;
+    }
+    const int m0 = w.m0, n0 = w.n0;
 
     // a thread's sums as 16-byte vectors q (q = (i NT + tt) 4 + v / 4):
     // vector q of thread tid at byte (q threads + tid) 16 of a partial slot
@@ -688,23 +821,27 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
     const int passes = BM * rs > C::kLds ? 2 : 1, prow = BM / passes;
     for (int ps = 0; ps < passes; ps++) {
         barrier();
+        if (!f32_out) {
+            // one pass (prow = BM)
+            if (ep.out_dt == DT_BF16) stage16<C, EPI, DT_BF16>(lds, rs, acc, ep, n0, N, wave, c, h);
+            else stage16<C, EPI, DT_F16>(lds, rs, acc, ep, n0, N, wave, c, h);
+        } else {
 #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            if (i * 32 / prow != ps) continue;
+            for (int i = 0; i < MT; i++) {
+                if (i * 32 / prow != ps) continue;
 #pragma unroll
-            for (int tt = 0; tt < NT; tt++) {
-                const int nl = wave * C::WN + 32 * tt + c;  // column within the tile
-                const int n = n0 + nl;
+                for (int tt = 0; tt < NT; tt++) {
+                    const int nl = wave * C::WN + 32 * tt + c;  // column within the tile
+                    const int n = n0 + nl;
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int ml = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3) - ps * prow;
-                    float o = acc[i][tt][v];
-                    if constexpr (EPI) {
-                        if (n < N) o = apply_epilogue(ep, (size_t)n, o);
+                    for (int v = 0; v < 16; v++) {
+                        const int ml = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3) - ps * prow;
+                        float o = acc[i][tt][v];
+                        if constexpr (EPI) {
+                            if (n < N) o = apply_epilogue(ep, (size_t)n, o);
+                        }
+                        *reinterpret_cast<float*>(lds + ml * rs + nl * 4) = o;
                     }
-                    uint8_t* d = lds + ml * rs + nl * esz;
-                    if (f32_out) *reinterpret_cast<float*>(d) = o;
-                    else *reinterpret_cast<uint16_t*>(d) = ep.out_dt == DT_BF16 ? f32_to_bf16(o) : f32_to_f16(o);
                 }
             }
         }
@@ -758,8 +895,9 @@ template <class C, bool EPI>
 LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
     if (planned(a, "qgemm_rw_kernel")) return LuxStatus::Ok;
     auto kern = qgemm_rw_kernel<C, EPI>;
+    constexpr int kLdsMax = C::kLds + (kStageAbove<C> ? kHandLds<C> : 0);
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
     if (attr != hipSuccess) return LuxStatus::Internal;
     const int mtiles = (a.M + C::BM - 1) / C::BM, ntiles = (a.N + BN - 1) / BN;
     const int tiles = mtiles * ntiles, KT = a.K / BK;
@@ -772,10 +910,17 @@ LuxStatus launch_e(const QmmArgs& a, hipStream_t st) {
                                    a.ws_bytes >= split::kPartOffset + (size_t)r * (C::BM * BN * 4)
                                ? tiles - r
                                : tiles;
-    const int blocks = nsplit > 1 ? tiles * nsplit : tiles + (tiles - split_from);
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(C::kThreads), C::kLds, st, static_cast<const uint16_t*>(a.x), a.wq,
+    const int units = nsplit > 1 ? tiles * nsplit : tiles + (tiles - split_from);
+    // one block per CU where there are more units than CUs and the
+    // hand-over's stores apply: 16-bit output in whole 16-byte chunks at
+    // 31-bit offsets (chunks past the end are dropped by offset)
+    const bool persist = nsplit == 1 && units > kCUs && a.out_dtype != DT_F32 && (((uintptr_t)a.y) & 15) == 0 &&
+                         a.N % 8 == 0 && (size_t)a.M * a.N * 2 < 0x80000000ull;
+    const int blocks = persist ? kCUs : units;
+    const int lds = persist ? kLdsMax : C::kLds;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(C::kThreads), lds, st, static_cast<const uint16_t*>(a.x), a.wq,
                        a.scales, a.biases, a.y, a.M, a.K, a.N, a.epi(), mtiles, ntiles, split_from, nsplit, a.ws,
-                       a.epoch);
+                       a.epoch, units);
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }
 

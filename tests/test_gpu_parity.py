@@ -651,6 +651,48 @@ def test_gemm_split_last_round(ctx, oracle):
                 assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), "repeat differs"
 
 
+PERSISTENT_CASES = [
+    # M, K, N, bits, gs, x, scales: more 128 x 256 tiles than CUs with a
+    # 16-bit output, so one block per CU runs several units in turn
+    (2000, 1024, 4360, 4, 64, BF16, BF16),   # 288 tiles: 64 blocks go on from a whole tile to a K half
+    (1000, 2048, 16136, 8, 128, F16, F16),   # 512 tiles, two per block; 8-bit: staged in the rings
+    (2048, 1024, 8200, 4, 32, F16, F32),     # 512 tiles + 16 split; f32 scales
+]
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES, ids=lambda c: f"M{c[0]}K{c[1]}N{c[2]}b{c[3]}")
+def test_rw_gemm_persistent_parity(ctx, oracle, case):
+    """The register-W GEMM on one block per CU, each block running units b,
+    b + 256, ...: a finished tile is staged and stored while the next
+    unit's first transfers land.  Whole outputs against the oracle's
+    dequantize-to-T form: ragged M (the last M tile's rows past M are
+    dropped by offset), ragged N (N % 256 != 0), the hand-over into a split
+    K half, both 16-bit outputs, and the fused output stage (bias and
+    activation applied in the hand-over's staging)."""
+    from mlx_amd import runtime
+    O = oracle
+    M, K, N, bits, gs, xd, sbd = case
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=7100 + N)
+    acc = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, F32, variant="omp", w_round=xd)
+    od = xd
+    y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od, KERNELS["gemm"])
+    check_output(O, y, O.from_f32(acc, od), od, f"persistent M{M} N{N} out{od}")
+    bias = O.from_f32(O.rng_normal(N, seed=7200 + N), F32)
+    act = 2 if bits == 4 else 3  # silu / gelu
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    bb = ctx.upload(bias)
+    try:
+        out = ctx.alloc(M * N * runtime.esize(od))
+        print(f"[case] persistent fused M={M} K={K} N={N} act={act} out={od}", flush=True)
+        ctx.quantized_matmul_fused(*bufs, bb, out, M, K, N, gs, bits, xd, sbd, F32, od, act)
+        yf = out.download(runtime.np_dtype(od), (M, N))
+        out.free()
+        check_output(O, yf, O.fused_epilogue(acc, bias, F32, act, od), od, f"persistent fused act{act}")
+    finally:
+        for t in bufs + [bb]:
+            t.free()
+
+
 # ---- fused output stage (bias + activation in the kernel's store) ---------
 
 FUSED_CASES = [
