@@ -561,10 +561,11 @@ __device__ __forceinline__ void stage16(uint8_t* dst, int rs, const f32x16 (&acc
 }
 
 // a 16-bit output tile handed over in a persistent grid: 16-byte chunks per
-// thread (chunk j of thread tid: row tid / 32 + 16 j, columns 8 (tid % 32)
-// ..+8), and the LDS above the rings where it is staged half its rows at a
-// time while the next unit's first transfers land -- where that fits; else
-// it is staged in the rings before those transfers are issued
+// thread (chunk j of thread tid: row tid / 32 + j kThreads / 32, columns
+// 8 (tid % 32) ..+8), and the LDS above the rings where it is staged half
+// its rows at a time while the next unit's first transfers land -- where
+// that fits; else it is staged in the rings before those transfers are
+// issued
 template <class C>
 constexpr int kHand = C::BM * BN * 2 / 16 / C::kThreads;
 template <class C>
@@ -577,6 +578,7 @@ constexpr bool kStageAbove = C::kLds + kHandLds<C> <= 160 * 1024;
 template <class C, bool EPI, int P>
 __device__ __forceinline__ void hand_half(uint8_t* hs, int rs, const f32x16 (&acc)[C::MT][C::NT], const Epilogue& ep,
                                           int n0, int N, int wave, int c, int h, int tid, u4 (&val)[kHand<C>]) {
+    static_assert(C::MT % 2 == 0 && kHand<C> % 2 == 0, "halves of whole 32-row tiles and chunk rounds");
     constexpr int I0 = P * C::MT / 2, I1 = I0 + C::MT / 2, kHalf = kHand<C> / 2;
     if (ep.out_dt == DT_BF16) stage16<C, EPI, DT_BF16, I0, I1>(hs, rs, acc, ep, n0, N, wave, c, h);
     else stage16<C, EPI, DT_F16, I0, I1>(hs, rs, acc, ep, n0, N, wave, c, h);
@@ -697,7 +699,7 @@ __global__ __launch_bounds__(C::kThreads, 1) void qgemm_rw_kernel(
             __builtin_amdgcn_make_buffer_rsrc(y, 0, (int)((uint32_t)M * (uint32_t)N * 2u), 0x00020000);
 #pragma unroll
         for (int j = 0; j < kHand<C>; j++) {
-            const int m = mo + (tid >> 5) + 16 * j, n = no + (tid & 31) * 8;
+            const int m = mo + (tid >> 5) + C::kThreads / 32 * j, n = no + (tid & 31) * 8;
             const uint32_t off = m < M && n < N ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * 2u : 0x80000000u;
             __builtin_amdgcn_raw_buffer_store_b128(val[j], yr, off, 0, 0);
         }
