@@ -666,16 +666,18 @@ extern "C" __attribute__((visibility("default"))) const char* lux_gpu_quantized_
     if (lux_hip_qmm_validate(M, K, N, group_size, bits, x_dtype, sb_dtype, out_dtype, kernel) != LUX_BACKEND_OK)
         return nullptr;
     if (M == 0 || N == 0) return "";
-    static uint8_t stand_in;
+    // never read or written; aligned like a device allocation, so that a
+    // launcher that chose by alignment would choose as for real buffers
+    alignas(256) static uint8_t stand_in[256];
     const char* name = nullptr;
     lxq::QmmArgs a;
-    a.x = a.scales = a.biases = &stand_in;
+    a.x = a.scales = a.biases = stand_in;
     a.wq = nullptr;
-    a.y = &stand_in;
+    a.y = stand_in;
     a.M = M; a.K = K; a.N = N; a.group_size = group_size; a.bits = bits;
     a.x_dtype = x_dtype; a.sb_dtype = sb_dtype; a.out_dtype = out_dtype;
     // a context's workspace
-    a.ws = &stand_in;
+    a.ws = stand_in;
     a.ws_bytes = lxq::kSplitWorkspaceBytes;
     a.epoch = 1u;
     a.plan = &name;
