@@ -6,7 +6,9 @@ context's workspace), and within the output gate of the oracle.  Two calls
 in a row share the scratch, the second with a smaller input; the first two
 run the split-K GEMM with its parts meeting in the scratch, the next two the
 large GEMM with the two K halves of its tiles meeting there, so a counter or
-flag left nonzero by one call would break the next.
+flag left nonzero by one call would break the next; the fifth runs the large
+GEMM on one block per CU (more tiles than CUs, 16-bit output), its blocks
+going on from a whole tile to a K half.
 """
 import ctypes
 import os
@@ -24,6 +26,7 @@ CALLS = [
     (17, 1152, 200, 4, 32, BF16, BF16, F32, 2),    # split-K GEMM, 3 K parts, 6 blocks
     (512, 1024, 1024, 4, 64, BF16, BF16, F32, 2),  # large GEMM, 16 tiles, each in two K halves
     (300, 512, 200, 4, 64, F16, F16, F16, 2),      # large GEMM, 4 ragged tiles, each in two K halves
+    (2000, 1024, 4360, 4, 64, BF16, BF16, BF16, 2),  # large GEMM, one block per CU: 288 ragged tiles, 32 in K halves
     (1, 4096, 512, 4, 64, F16, F16, F16, 0),       # a GEMV: no scratch
 ]
 
@@ -98,21 +101,21 @@ def test_noalloc_matches_context_op(ctx, oracle):
 
 
 def test_noalloc_back_to_back(ctx, oracle):
-    """The split-K and split-last-round calls of CALLS enqueued on one stream
-    with no synchronize between them (the scratch's counters and flags must
-    be back at zero when the next call starts), then each output against the
-    context op on the same inputs, bit for bit."""
+    """The split-K, split-last-round and persistent calls of CALLS enqueued
+    on one stream with no synchronize between them (the scratch's counters
+    and flags must be back at zero when the next call starts), then each
+    output against the context op on the same inputs, bit for bit."""
     from mlx_amd import runtime
     O = oracle
     f = _entry()
     hip = _Hip()
     stream = ctypes.c_void_p()
     hip.ck(hip.L.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
-    calls, held = CALLS[:4] * 2, []
+    calls, held = CALLS[:5] * 2, []
     try:
         for i, (M, K, N, bits, gs, xd, sbd, od, kern) in enumerate(calls):
             print(f"[case] noalloc back-to-back call {i}: M={M} K={K} N={N} b={bits} kernel={kern}", flush=True)
-            x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=700 + i % 4)
+            x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=700 + i % 5)
             ptrs = [hip.upload(np.ascontiguousarray(a)) for a in (x, w_q, s, b)]
             out = hip.alloc(M * N * runtime.esize(od))
             held.append((ptrs, out, (x, w_q, s, b), (M, K, N, bits, gs, xd, sbd, od, kern)))
