@@ -7,13 +7,16 @@
 // A block is 4 waves, wave w owns R consecutive rows (R = 4 or 7, whichever
 // spreads the blocks more evenly over the 256 CUs).  Every load is issued
 // at the start, straight into registers:
+//   0. with R = 7 and the wave's own x: the first row's codes (below), so
+//      that the HBM stream is under way while steps 1-2 pass through the
+//      CU's queue;
 //   1. x: the lane's code chunks' x values (L2-resident after first touch),
 //      or, for the widths and types where it measured faster, the block's
 //      x once (16 bytes per thread), shared through LDS after the codes are
 //      issued;
 //   2. the wave's R scale rows and R bias rows, as whole 16-byte chunks;
 //   3. a block barrier, so that the x and scale requests of all four waves
-//      enter the CU's vector-memory queue ahead of every code request;
+//      enter the CU's vector-memory queue ahead of every other code request;
 //   4. the codes: for each row, NI wave loads of SPAN contiguous bytes (lane
 //      l takes the l-th 16- or 12-byte chunk, 4*WPI bytes = NC codes), with
 //      the non-temporal cache policy.  Each wave instruction covers whole
@@ -314,6 +317,47 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
 #pragma unroll
     for (int i = 0; i < NI; i++) ok[i] = (uint32_t)(i * 64 + lane) * NC < (uint32_t)K;
 
+    // row r's codes: whole lines, non-temporal (rows past N re-read row
+    // N - 1, never stored)
+    constexpr bool XSH = !(BITS == 4 && TX != DT_F32);
+    uint32_t w[R][NI][WPI];
+    auto row_loads = [&](int r) {
+        // the block's rows (the compiler computes this once, where the
+        // first row's loads are issued)
+        const size_t wleft = (size_t)(N - nb0) * row_bytes;
+        const auto wr = buf_rsrc(reinterpret_cast<const uint8_t*>(wq) + (size_t)nb0 * row_bytes,
+                                 (uint32_t)(wleft < 0x7fffffffu ? wleft : 0x7fffffffu));
+        const int n = n0 + r < N ? n0 + r : N - 1;
+        const uint32_t soff = (uint32_t)(n - nb0) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const uint32_t voff = ok[i] ? (uint32_t)(i * C::SPAN + lane * 4 * WPI) : kZeroOff;
+            if constexpr (WPI == 4) {
+                const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, kCachePolicyNT);
+                w[r][i][0] = v.x; w[r][i][1] = v.y; w[r][i][2] = v.z; w[r][i][3] = v.w;
+            } else {
+                const v3u32 v = __builtin_amdgcn_raw_buffer_load_b96(wr, voff, soff, kCachePolicyNT);
+                w[r][i][0] = v.x; w[r][i][1] = v.y; w[r][i][2] = v.z;
+            }
+        }
+        // issue the rows in order: loads return in issue order and the
+        // rows are computed in this order (left free, the scheduler
+        // interleaved the rows' loads, and the first rows' arithmetic then
+        // waited for most of the stream: 7.9 against 7.5 us at c1)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // ---- 0. 7-row waves that load their own x: the first row's codes go
+    // out ahead of x and the scale rows, so the HBM stream has begun while
+    // those pass through the CU's queue.  Measured (same box, back-to-back
+    // launches, µs): c1 7.29 -> 7.14 (f16 x), 7.62 -> 7.39 (bf16 x); the
+    // first two rows 7.16; only the row's first 1 KB 7.34; the scale rows
+    // also ahead of x 7.42; no block barrier 7.70.  With 4-row waves (N =
+    // 4096, 11008) or x shared through LDS (c0, c4 3/6-bit) it was 0.16-0.63
+    // slower, so they keep x first. ----
+    constexpr bool kEarlyRow = !XSH && R == 7;
+    if constexpr (kEarlyRow) row_loads(0);
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- 1. x.  XSH: once per block, thread t loading 16-byte chunks t,
     // t + 256, ... of the 4096 codes' x (past K: zeros), shared through LDS
     // (step 6); else each wave loads its lanes' chunks.  Measured (same box,
@@ -322,7 +366,6 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
     // 3- and 8-bit, but 7.67 against 7.37-7.54 at configs[1] (4-bit, f16 x),
     // where the block barrier before the x reads costs more than the queue
     // time of the per-wave copies. ----
-    constexpr bool XSH = !(BITS == 4 && TX != DT_F32);
     constexpr int kXQ = XSH ? 4096 * XE / 4096 : 1;  // 16-byte chunks per thread
     const int tid = threadIdx.x;
     uint32_t xq[kXQ][4];
@@ -377,37 +420,13 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // ---- 3. every wave's x and scale requests ahead of any code request ----
+    // ---- 3. every wave's x and scale requests ahead of its (other) code
+    // requests ----
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    // ---- 4. codes: whole lines, non-temporal ----
-    uint32_t w[R][NI][WPI];
-    {
-        const size_t wleft = (size_t)(N - nb0) * row_bytes;
-        const auto wr = buf_rsrc(reinterpret_cast<const uint8_t*>(wq) + (size_t)nb0 * row_bytes,
-                                 (uint32_t)(wleft < 0x7fffffffu ? wleft : 0x7fffffffu));
+    // ---- 4. the (other) rows' codes ----
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int n = n0 + r < N ? n0 + r : N - 1;
-            const uint32_t soff = (uint32_t)(n - nb0) * row_bytes;
-#pragma unroll
-            for (int i = 0; i < NI; i++) {
-                const uint32_t voff = ok[i] ? (uint32_t)(i * C::SPAN + lane * 4 * WPI) : kZeroOff;
-                if constexpr (WPI == 4) {
-                    const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, kCachePolicyNT);
-                    w[r][i][0] = v.x; w[r][i][1] = v.y; w[r][i][2] = v.z; w[r][i][3] = v.w;
-                } else {
-                    const v3u32 v = __builtin_amdgcn_raw_buffer_load_b96(wr, voff, soff, kCachePolicyNT);
-                    w[r][i][0] = v.x; w[r][i][1] = v.y; w[r][i][2] = v.z;
-                }
-            }
-            // issue the rows in order: loads return in issue order and the
-            // rows are computed in this order (left free, the scheduler
-            // interleaved the rows' loads, and the first rows' arithmetic then
-            // waited for most of the stream: 7.9 against 7.5 us at c1)
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
+    for (int r = kEarlyRow ? 1 : 0; r < R; r++) row_loads(r);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 5. the scale rows into the wave's LDS area (every lane writes,
