@@ -235,9 +235,10 @@ struct Lay {
     static constexpr int kNWI = BITS * kSW / 4;         // W DMAs per column tile and W issue
     static constexpr int kNSS = 2 * NT * kNS;           // scale + bias DMAs per super-step
     static constexpr int kNWS = NT * kNWI + kNSS;       // DMAs of the largest W issue
-    // loads younger than X(q) when step q waits: the x and W DMAs issued in
-    // steps q - kRX + 2 .. q, at most (kRX - 1) x-issues and one W issue
-    static constexpr int kMaxWait = (kRX - 1) * (kNX + NT * kNWI) + kNSS;
+    // loads younger than X(q) when step q waits: the W DMAs issued in steps
+    // q - kRX + 1 .. q and the x DMAs of steps q - kRX + 2 .. q: kRX - 1
+    // x issues, a slot's W at most once per kSW steps, one scale super-step
+    static constexpr int kMaxWait = (kRX - 1) * kNX + (kRX + kSW - 1) / kSW * NT * kNWI + kNSS;
     // W super-steps resident: 3 (two in flight) unless LDS or vmcnt say 2
     static constexpr int kWaveBytes3 = kRX * kXS + 3 * (kWS + 2 * kSS);
     static constexpr int kRW = (!kHW && 4 * kWaveBytes3 <= 160 * 1024) ? 3 : 2;  // scale slots (and W slots unless kHW)
@@ -314,11 +315,13 @@ __device__ __forceinline__ void issue_w(const Ctx<BITS, SB, MT, NT, GS>& c, int 
         }
 }
 
-// DMAs of the W and scale issues among steps q - kRX + 2 .. q (P = q % 4)
+// DMAs of the W and scale issues among steps q - kRX + 1 .. q (P = q % 4);
+// steps before 0 count as the steady state would issue them, which the
+// prologue follows
 template <class L, int NT, int P>
 constexpr int young_w() {
     int n = 0;
-    for (int d = 0; d <= L::kRX - 2; d++) {
+    for (int d = 0; d <= L::kRX - 1; d++) {
         const int p = ((P - d) % 4 + 4) % 4;
         if (p % L::kSW == 0) n += NT * L::kNWI;
         if (p == 0) n += L::kNSS;
@@ -332,10 +335,17 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
                                      int nq) {
     using L = Lay<BITS, SB, MT, NT, GS>;
     const int u = q >> 2;
-    // issue: W/scales of super-step u + kRW - 1 (at P == 0), x of step q + kRX - 1
-    // (past the part's end they repeat its last super-step / step: counts stay
-    // fixed), once the previous step's reads of the refilled slots are done
+    // issue: x of step q + kRX - 1, then W/scales of super-step u + kRW - 1
+    // (at P == 0) (past the part's end they repeat its last step / super-step:
+    // counts stay fixed), once the previous step's reads of the refilled slots
+    // are done.  x goes first: its wait comes kRX - 1 steps later, W's at
+    // least 4 (M = 64, K = 4096, N = 11008, 3-bit: 17.80 -> 17.38 us; 1-2 %
+    // on the other shapes measured)
     wait_lds_reads();
+    {
+        const int qx = q + L::kRX - 1;
+        issue_x(c, qx < nq ? qx : nq - 1);
+    }
     if constexpr (L::kHW) {
         // unit g + kLead into the slot unit g - 1 used, at the first step of
         // unit g; at P == 0 also the scales of super-step u + 1
@@ -351,13 +361,9 @@ __device__ __forceinline__ void step(f32x16 (&acc)[NT][MT], const Ctx<BITS, SB, 
         const int uw = u + L::kRW - 1, ul = (nq >> 2) - 1;
         issue_w(c, uw < ul ? uw : ul);
     }
-    {
-        const int qx = q + L::kRX - 1;
-        issue_x(c, qx < nq ? qx : nq - 1);
-    }
-    // X(q) (and the older W(u)) landed: younger are the issues of steps
-    // q - kRX + 2 .. q: kRX - 1 x issues, plus the W issue of the one of
-    // those steps that starts a super-step, if any (P <= kRX - 2; kRX <= 5)
+    // X(q) (and the older W(u)) landed: younger are the W issues of steps
+    // q - kRX + 1 .. q (X(q) went first in step q - kRX + 1) and the x
+    // issues of steps q - kRX + 2 .. q
     static_assert(L::kRX >= 2 && L::kRX <= 4, "W issued 4 steps ahead: older than the x awaited");
     // the W issues of those steps: a slot's W at each step with P % kSW == 0,
     // the scales (and, for whole slots, the W) at the one with P == 0
@@ -468,15 +474,27 @@ __global__ __launch_bounds__(64 * kWaves) void qgemm_small_kernel(
     uint8_t* lw = lds + (size_t)wave * L::kWaveBytes;
 
     // prologue: the issues of steps -kRX+1 .. -1 and super-steps up to kRW - 2
-    // in the same order the steady state keeps (missing ones repeat step 0)
+    // in the order the steady state keeps, which the waits of steps 0 ..
+    // kRX - 2 count on: first what it issues before step -kRX + 1 (the W and
+    // scale slots, the part-super-step units g with (g - kLead) kSW < 1 - kRX),
+    // then step s = -kRX + 1 .. -1: x of step s + kRX - 1, then the unit of s
+    // where s % kSW == 0.  (All units issued ahead of x once let step 0 of
+    // 8-bit, f32-scale, group-32 tiles read x before it landed.)
     if constexpr (L::kHW) {
 #pragma unroll
-        for (int g = 0; g < L::kLead; g++) issue_wh(c, g);  // a part has at least one super-step: 4 / kSW units
+        for (int g = 0; g < L::kLead; g++)  // a part has at least one super-step: 4 / kSW units
+            if ((g - L::kLead) * L::kSW < 1 - L::kRX) issue_wh(c, g);
     }
 #pragma unroll
     for (int uu = 0; uu < L::kRW - 1; uu++) issue_w(c, uu < (nq >> 2) - 1 ? uu : (nq >> 2) - 1);
 #pragma unroll
-    for (int qq = 0; qq < L::kRX - 1; qq++) issue_x(c, qq < nq - 1 ? qq : nq - 1);
+    for (int qq = 0; qq < L::kRX - 1; qq++) {
+        issue_x(c, qq < nq - 1 ? qq : nq - 1);
+        if constexpr (L::kHW) {
+            constexpr int s0 = 1 - L::kRX;  // step of x(qq) is s0 + qq
+            if ((s0 + qq) % L::kSW == 0) issue_wh(c, (s0 + qq) / L::kSW + L::kLead);
+        }
+    }
     // the steady state's W issue of super-step kRW - 1 happens in step 0
 
     f32x16 acc[NT][MT];

@@ -573,6 +573,40 @@ def test_ring_kernels_repeat_full_grid(ctx, oracle, M, K, N, bits, gs, xd, kern)
             t.free()
 
 
+@pytest.mark.parametrize("M,K,N,bits,gs,xd,sbd", [
+    (32, 4096, 11008, 8, 32, BF16, F32),   # quarter-super-step W slots, three x slots
+    (32, 4096, 11008, 8, 64, F16, F16),    # half-super-step W slots, three x slots
+    (64, 4096, 11008, 8, 64, F16, F16),    # quarter-super-step W slots, two x slots
+])
+def test_small_gemm_first_steps_repeat(ctx, oracle, M, K, N, bits, gs, xd, sbd):
+    """The two-tile small-M GEMM on part-super-step W slots over a full grid,
+    48 launches in a row: the first equals the oracle and every one the first
+    bit for bit.  The waits of a wave's first steps count the DMAs issued
+    after its x as the steady state orders them; a prologue that issued every
+    W unit ahead of x left the first step of the 8-bit, f32-scale, group-32
+    tiles able to read x before it landed (4 to 12 distinct outputs in 64
+    launches)."""
+    O = oracle
+    from mlx_amd import abi
+    x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=4100 + M + gs)
+    want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, F32, variant="omp", w_round=xd)
+    bufs = [ctx.upload(a) for a in (x, w_q, s, b)]
+    out = ctx.alloc(M * N * 4)
+    try:
+        print(f"[case] small gemm first steps M={M} K={K} N={N} b={bits} g={gs} s={sbd}", flush=True)
+        first = None
+        for rep in range(48):
+            ctx.quantized_matmul(*bufs, out, M, K, N, gs, bits, xd, sbd, F32, abi.KERNEL_GEMM)
+            y = out.download(np.float32, (M, N))
+            if first is None:
+                check_output(O, y, want, F32, "small gemm first steps")
+                first = y
+            assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), f"launch {rep} differs from launch 0"
+    finally:
+        for t in bufs + [out]:
+            t.free()
+
+
 def test_gemm_shape_limits(ctx, oracle):
     """K not a multiple of 256: an explicit GEMM request is NOT_SUPPORTED,
     AUTO picks the GEMV (exact weights) for any M."""
