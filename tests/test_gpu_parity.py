@@ -475,8 +475,8 @@ def test_small_gemm_parity(ctx, oracle, bits, xd, sbd, od):
 def test_small_gemm_two_tiles_parity(ctx, oracle, bits, xd, sbd, od):
     """Past 256 column tiles of 32 (N > 8192) the small-M GEMM runs two tiles
     per block where their rings fit (6- and 8-bit codes through half- or
-    quarter-super-step W slots; blocks with f32 scales at group 32 and 8-bit
-    codes, or 6-bit ones at two M tiles, keep one tile and run two rounds):
+    quarter-super-step W slots; 5-, 6- and 8-bit codes with f32 scales at
+    group 32 and two M tiles keep one tile and run two rounds):
     ragged N with the last block's second tile wholly past N (N = 8200),
     group sizes 32 (the rings fill the 160 KB exactly for 4-bit codes with
     f32 scales and 8-bit ones with 16-bit scales), 64 and 128, one and two M
