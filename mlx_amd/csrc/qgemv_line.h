@@ -4,8 +4,8 @@
 // Included after qgemv_impl.h (it uses its buffer, operand and reduction
 // helpers) by the per-bit-width translation units.
 //
-// A block is 4 waves, wave w owns R consecutive rows (R = 4 or 7, whichever
-// spreads the blocks more evenly over the 256 CUs).  Every load is issued
+// A block is 4 waves, wave w owns R consecutive rows (R = 4, 6 or 7: see
+// line_rows below).  Every load is issued
 // at the start, straight into registers:
 //   0. with R = 7 and the wave's own x: the first row's codes (below), so
 //      that the HBM stream is under way while steps 1-2 pass through the
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(256) void qgemv_line_kernel(
     constexpr int NC = C::NC, WPI = C::WPI;
     constexpr int XW = NC * XE / 4;  // 32-bit words of x per chunk
     constexpr int NT = TWO ? 2 : 1;  // groups per chunk
-    static_assert(R == 4 || R == 7, "rows per wave");
+    static_assert(R == 4 || R == 6 || R == 7, "rows per wave");
     static_assert(NI * 64 * NC <= 4096, "the lanes' chunks lie in the block's copy of x");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -564,8 +564,36 @@ LuxStatus launch_line_q(const QmmArgs& a, hipStream_t st) {
     }
 }
 
+// Rows per wave for 2- to 4-bit codes with 16-bit x: of R = 7, 6, 4 the one
+// whose busiest CU holds the fewest rows (ceil(blocks / 256) blocks of 4R
+// rows), the larger R on a tie.  Measured against the rule above (same box,
+// bit-identical outputs, µs per launch, K = 4096 unless noted): N = 11008
+// 3-bit 6.29 -> 6.18 (R 6 against 4), 4-bit 6.31 -> 6.24, 2-bit 5.82 ->
+// 5.63, K = 2048 4.36 -> 4.23; N = 12288 4-bit 6.70 -> 6.54; N = 5120
+// 4-bit 4.35 -> 4.02, 3-bit 4.59 -> 4.10 (R 6 against 7).  Over the whole
+// R = 2..8 range at N = 11008 the time followed the busiest CU's rows (48
+// rows 6.2-6.8 us, 60 rows 7.2, 64 rows 7.6), fewer blocks winning a tie.
+// 6- and 8-bit codes were slower with R = 6 (8.45 -> 9.25, 9.43 -> 9.64)
+// and keep the rule above, as does f32 x (not measured).
+inline int line_rows_narrow(int N) {
+    int best = 4, best_rows = 1 << 30;
+    for (int R : {7, 6, 4}) {
+        const int blocks = (N + 4 * R - 1) / (4 * R);
+        const int rows = (blocks + 255) / 256 * 4 * R;
+        if (rows < best_rows) best = R, best_rows = rows;
+    }
+    return best;
+}
+
 template <int BITS, int TX, int SB, int NI, bool TWO>
 LuxStatus launch_line_r(const QmmArgs& a, hipStream_t st) {
+    if constexpr (BITS <= 4 && TX != DT_F32) {
+        switch (line_rows_narrow(a.N)) {
+        case 7: return launch_line_q<BITS, TX, SB, NI, TWO, 7>(a, st);
+        case 6: return launch_line_q<BITS, TX, SB, NI, TWO, 6>(a, st);
+        default: return launch_line_q<BITS, TX, SB, NI, TWO, 4>(a, st);
+        }
+    }
     if (line_rows7(a.N)) return launch_line_q<BITS, TX, SB, NI, TWO, 7>(a, st);
     return launch_line_q<BITS, TX, SB, NI, TWO, 4>(a, st);
 }

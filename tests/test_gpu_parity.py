@@ -91,6 +91,23 @@ def test_quantize_bit_exact(ctx, oracle, bits, gs):
 
 # ---- GEMV ---------------------------------------------------------------
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_line_gemv_six_rows(ctx, oracle, bits, xd, sbd, od):
+    """M = 1 on the whole-line GEMV where 2- to 4-bit codes with 16-bit x
+    take 6-row waves (24-row blocks leave the busiest CU the fewest rows):
+    N = 5120 (214 blocks, one per CU), 11000 (459 blocks, the last one
+    ragged), 12288 (512 blocks, two per CU) and 5130 at K = 960 (an odd
+    chunk count), every group size."""
+    O = oracle
+    for (K, N, gs) in [(4096, 5120, 64), (2048, 11000, 32), (4096, 12288, 128), (960, 5130, 32)]:
+        assert ctx.kernel_name(1, K, N, gs, bits, xd, sbd, od) == "qgemv_line_kernel"
+        x, w_q, s, b, _ = O.make_problem(1, K, N, bits, gs, xd, sbd, seed=bits * 53 + N)
+        y = run(ctx, x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od)
+        want = O.quantized_matmul(x, w_q, s, b, 1, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"line six rows b{bits} K{K} N{N} g{gs}")
+
+
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F32, F32, F32),
                                        (F16, F32, F32), (BF16, F16, F32)])
@@ -732,6 +749,7 @@ def test_rw_gemm_persistent_parity(ctx, oracle, case):
 FUSED_CASES = [
     # M, K, N, bits, gs, x dtype: AUTO routes each to a different kernel
     (1, 4096, 300, 4, 64, F16),     # whole-line GEMV
+    (1, 4096, 5120, 3, 64, BF16),   # whole-line GEMV, 6-row waves
     (1, 14336, 70, 4, 64, BF16),    # split-K GEMV
     (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
     (2, 4096, 40, 3, 64, F16),      # stream GEMV (two rows of x, 3-bit)
