@@ -141,20 +141,24 @@ def per_launch_us(hip, stream, step, steps):
             "p90": round(float(np.percentile(d, 90)), 3), "first": [round(float(v), 3) for v in d[:3]]}
 
 
-def time_launches(hip, stream, step, steps, warmup):
+def time_launches(hip, stream, step, steps, warmup, loop=None):
     """Warm-up (warm(): at least `warmup` launches and WARM_S seconds), then
     exactly `steps` launches back to back on `stream` between a synchronize
     on each side; returns host wall time of the region and the HIP-event
     time per launch, then the per-launch durations of the same launches run
     once more (per_launch_us).  step(i) enqueues launch i (rotating over the
-    weight copies itself)."""
+    weight copies itself); loop(first, n), where given, enqueues launches
+    first .. first + n - 1 from C and issues the timed ones."""
     warm(hip, stream, step, warmup)
     e0, e1 = hip.event(), hip.event()
     hip.sync(stream)
     t0 = time.perf_counter()
     hip.record(e0, stream)
-    for i in range(steps):
-        step(i)
+    if loop is not None:
+        loop(0, steps)
+    else:
+        for i in range(steps):
+            step(i)
     hip.record(e1, stream)
     hip.sync(stream)
     wall = time.perf_counter() - t0
@@ -294,7 +298,21 @@ def bench_qmm(ctx, hip, M, K, N, bits, gs, xd, sbd, od, steps, warmup, kernel, c
         wq, s, b = sets[i % copies]
         ctx.quantized_matmul(xb, wq, s, b, out, M, K, N, gs, bits, xd, sbd, od, kernel)
 
-    r = time_launches(hip, stream, step, steps, max(warmup, copies))
+    # the timed launches: the same op through the same table entry, called
+    # from a C loop (a Python call per launch costs ~6 us of host time, about
+    # as long as the M = 1 kernel runs, so a slow host would leave the GPU
+    # idle between launches)
+    L = ceiling_lib()
+    fn = ctypes.cast(ctx.q.op_quantized_matmul_ex, ctypes.c_void_p)
+    handles = [(ctypes.c_void_p * copies)(*[st[j].handle for st in sets]) for j in range(3)]
+
+    def loop(first, n):
+        rc = L.lux_bench_qmm_loop(fn, ctx.handle, xb.handle, handles[0], handles[1], handles[2], copies,
+                                  out.handle, M, K, N, gs, bits, xd, sbd, od, kernel, first, n)
+        if rc != 0:
+            raise RuntimeError(f"op_quantized_matmul_ex failed in the C loop: {rc}")
+
+    r = time_launches(hip, stream, step, steps, max(warmup, copies), loop)
     r["graph_ms_per_launch"] = time_graph(hip, stream, step)
     r["steps"] = steps
     r["digest_match"] = dm
@@ -320,6 +338,10 @@ def ceiling_lib():
     L.lux_ceiling_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
     L.lux_ceiling_empty_loop.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.POINTER(ctypes.c_float)]
+    L.lux_ceiling_read_loop.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    L.lux_bench_qmm_loop.argtypes = [ctypes.c_void_p] * 3 + [ctypes.POINTER(ctypes.c_void_p)] * 3 + \
+        [ctypes.c_int, ctypes.c_void_p] + [ctypes.c_int] * 11
     L.lux_bench_rng_normal_f32.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
                                            ctypes.c_float]
     L.lux_bench_rng_u32.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64]
@@ -345,8 +367,13 @@ def ceiling_leg(ctx, hip, nbytes, steps, warmup, blocks):
         def empty(i):
             hip.ck(L.lux_ceiling_empty(blocks, sink, ctypes.c_void_p(stream)), "lux_ceiling_empty")
 
-        for name, fn in (("empty", empty), ("read", read)):
-            r = time_launches(hip, stream, fn, steps, warmup)
+        def read_loop(first, n):
+            # timed like the quantized matmul: the launches issued from C
+            hip.ck(L.lux_ceiling_read_loop(ctypes.c_void_p(base), stride, COPIES, nbytes, sink,
+                                           ctypes.c_void_p(stream), first, n), "lux_ceiling_read_loop")
+
+        for name, fn, loop in (("empty", empty, None), ("read", read, read_loop)):
+            r = time_launches(hip, stream, fn, steps, warmup, loop)
             g = time_graph(hip, stream, fn)
             us = r["event_ms_per_launch"] * 1e3
             out[name] = {"us_per_launch": round(us, 3), "graph_us_per_launch": round(g * 1e3, 3)}
@@ -725,7 +752,9 @@ def main():
                      "kernel_us_median": r["per_launch_us"]["median"], "per_launch_us": r["per_launch_us"],
                      "graph_us_per_launch": round(r["graph_ms_per_launch"] * 1e3, 3),
                      "graph_frac": round(wb / r["graph_ms_per_launch"] / 1e6 / HBM_PEAK_GBS, 4),
-                     "algorithmic_bytes": wb, "timing": "HIP events around the timed launches on the plugin stream"},
+                     "algorithmic_bytes": wb,
+                     "timing": "HIP events around the timed launches on the plugin stream, issued from a C loop "
+                               "through the plugin's op table"},
     }
     if not args.no_ceiling:
         line["ceiling"] = ceiling_leg(ctx, hip, wb, args.steps, args.warmup, 512)

@@ -71,6 +71,22 @@ __attribute__((visibility("default"))) int lux_ceiling_read(const void* buf, uin
     return (int)hipGetLastError();
 }
 
+// Launches i = first .. first + n - 1 of the plain read, launch i reading
+// the `bytes` bytes at base + (i % copies) * stride, from this C loop (the
+// way bench.py issues the timed quantized-matmul launches).  Returns the
+// first hipError_t met.
+__attribute__((visibility("default"))) int lux_ceiling_read_loop(const void* base, uint64_t stride, int copies,
+                                                                 uint64_t bytes, void* sink, void* stream, int first,
+                                                                 int n) {
+    if (copies <= 0 || n < 0 || first < 0) return (int)hipErrorInvalidValue;
+    for (int i = first; i < first + n; i++) {
+        const int rc = lux_ceiling_read(static_cast<const uint8_t*>(base) + (uint64_t)(i % copies) * stride, bytes,
+                                        sink, stream);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
 // `n` launches of the empty kernel (`blocks` blocks) issued back to back
 // from this C loop, between two events on `stream`: the per-launch floor
 // without a Python call per launch.  *ms_out: the events' elapsed time.
@@ -93,6 +109,32 @@ __attribute__((visibility("default"))) int lux_ceiling_empty_loop(int n, int blo
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     return (int)e;
+}
+
+// The plugin's op_quantized_matmul_ex (lux_gpu_quant_backend.h), called
+// through the pointer the quant table holds: opaque context and buffer
+// handles, then the shape, the dtypes and the kernel choice as ints.
+typedef int (*LuxQmmExFn)(void* ctx, void* x, void* w_q, void* scales, void* biases, void* out, int M, int K,
+                          int N, int group_size, int bits, int x_dtype, int sb_dtype, int out_dtype, int kernel);
+
+// Calls i = first .. first + n - 1 of the op from this C loop, call i on
+// weight set i % copies (w_q[], scales[], biases[] hold `copies` handles),
+// the way a C caller drives the op, with no Python call per launch: what
+// bench.py times.  Returns the op's first non-zero status, else 0.
+__attribute__((visibility("default"))) int lux_bench_qmm_loop(void* fn, void* ctx, void* x, void* const* w_q,
+                                                              void* const* scales, void* const* biases,
+                                                              int copies, void* out, int M, int K, int N,
+                                                              int group_size, int bits, int x_dtype, int sb_dtype,
+                                                              int out_dtype, int kernel, int first, int n) {
+    if (fn == nullptr || copies <= 0 || n < 0 || first < 0) return (int)hipErrorInvalidValue;
+    const LuxQmmExFn op = reinterpret_cast<LuxQmmExFn>(fn);
+    for (int i = first; i < first + n; i++) {
+        const int c = i % copies;
+        const int rc = op(ctx, x, w_q[c], scales[c], biases[c], out, M, K, N, group_size, bits, x_dtype, sb_dtype,
+                          out_dtype, kernel);
+        if (rc != 0) return rc;
+    }
+    return 0;
 }
 
 }  // extern "C"
