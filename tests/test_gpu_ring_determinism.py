@@ -1,0 +1,91 @@
+"""Repeat-launch determinism of the DMA-ring kernels over their layouts.
+
+The small-M GEMM (qgemm_small) and the mid-M GEMV (qgemv_mid) stage x, W and
+the scales in per-wave LDS rings filled by buffer->LDS transfers, and every
+step waits on a compile-time count of the transfers issued after the x it
+reads.  A count that is too large for some layout (code width, scale dtype,
+group size, one or two 32-row M tiles, one or two column tiles per block:
+each changes the ring's slots and the transfers per issue) lets a step read
+a slot before its data landed: the output then changes from launch to
+launch.  One such count was found this way (the first step of the 8-bit,
+f32-scale, group-32 two-tile blocks); the oracle comparisons elsewhere ran
+those shapes once and passed.
+
+Each case runs LAUNCHES launches back to back into separate output buffers
+(fp32, so that every bit of the sums shows), synchronizes once and checks
+that all of them equal the first bit for bit.  K = 1024 gives each wave one
+super-step, so the prologue's issues and the first steps' waits are most of
+the kernel.  The inputs are random codes with finite scales, biases and x:
+the oracle checks of these kernels are in test_gpu_parity.py.
+"""
+import numpy as np
+import pytest
+
+from qmm_util import BF16, F16, F32
+
+pytestmark = pytest.mark.gpu
+
+LAUNCHES = 32
+BITS = [2, 3, 4, 5, 6, 8]
+SB = [F16, BF16, F32]
+GROUPS = [32, 64, 128]
+
+
+def _values(rng, n, lo, hi, dtype):
+    v = rng.uniform(lo, hi, n).astype(np.float32)
+    if dtype == F32:
+        return v
+    if dtype == F16:
+        return v.astype(np.float16)
+    return (v.view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits (truncated)
+
+
+def _repeat(ctx, M, K, N, gs, bits, xd, sbd, kernel, name, seed):
+    from mlx_amd import abi, runtime
+    kern = abi.KERNEL_GEMM if kernel == "qgemm_small_kernel" else abi.KERNEL_GEMV
+    assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, F32, kern) == kernel, "case meant for " + kernel
+    rng = np.random.default_rng(seed)
+    x = _values(rng, M * K, -1.0, 1.0, xd)
+    w_q = rng.integers(0, 2**32, N * K * bits // 32, dtype=np.uint32)
+    s = _values(rng, N * (K // gs), 0.004, 0.02, sbd)
+    b = _values(rng, N * (K // gs), -0.2, -0.05, sbd)
+    ins = [ctx.upload(a) for a in (x, w_q, s, b)]
+    outs = [ctx.alloc(M * N * 4) for _ in range(LAUNCHES)]
+    try:
+        print(f"[case] {name}", flush=True)
+        for o in outs:
+            ctx.quantized_matmul(*ins, o, M, K, N, gs, bits, xd, sbd, F32, kern)
+        ctx.sync()
+        ys = [o.download(np.float32, (M, N)).view(np.uint32) for o in outs]
+    finally:
+        for t in ins + outs:
+            t.free()
+    assert np.isfinite(ys[0].view(np.float32)).all(), f"{name}: non-finite output"
+    bad = [i for i, y in enumerate(ys) if not np.array_equal(y, ys[0])]
+    assert not bad, f"{name}: launches {bad} differ from launch 0"
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("sbd", SB, ids=["sb_f16", "sb_bf16", "sb_f32"])
+def test_small_gemm_rings_repeat(ctx, bits, sbd):
+    """qgemm_small, every group size: one M tile with two column tiles per
+    block where they fit (M = 24, N = 8400: 263 column tiles), two M tiles
+    likewise (M = 64) and two M tiles with one column tile (M = 40, N =
+    2000)."""
+    xd = BF16 if sbd == BF16 else F16
+    for gs in GROUPS:
+        for M, N in [(24, 8400), (64, 8400), (40, 2000)]:
+            name = f"small gemm b{bits} g{gs} sb{sbd} M{M} N{N}"
+            _repeat(ctx, M, 1024, N, gs, bits, xd, sbd, "qgemm_small_kernel", name, 9000 + 7 * bits + M + gs)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("sbd", SB, ids=["sb_f16", "sb_bf16", "sb_f32"])
+def test_mid_gemv_rings_repeat(ctx, bits, sbd):
+    """qgemv_mid (M = 9..16 rows of x), every group size, K = 1024 and
+    4096."""
+    xd = BF16 if sbd == BF16 else F16
+    for gs in GROUPS:
+        for M, K in [(9, 1024), (16, 1024), (12, 4096)]:
+            name = f"mid gemv b{bits} g{gs} sb{sbd} M{M} K{K}"
+            _repeat(ctx, M, K, 4100, gs, bits, xd, sbd, "qgemv_mid_kernel", name, 9500 + 5 * bits + M + gs)
