@@ -1,4 +1,5 @@
-"""Repeat-launch determinism of the DMA-ring kernels over their layouts.
+"""Repeat-launch determinism over the layouts of the kernels whose waits or
+cross-block meetings depend on them.
 
 The small-M GEMM (qgemm_small) and the mid-M GEMV (qgemv_mid) stage x, W and
 the scales in per-wave LDS rings filled by buffer->LDS transfers, and every
@@ -12,11 +13,19 @@ f32-scale, group-32 two-tile blocks); the oracle comparisons elsewhere ran
 those shapes once and passed.
 
 Each case runs LAUNCHES launches back to back into separate output buffers
-(fp32, so that every bit of the sums shows), synchronizes once and checks
+(fp32, so that every bit of the sums shows, but for the register-W GEMM's
+persistent grid, which stores 16-bit outputs), synchronizes once and checks
 that all of them equal the first bit for bit.  K = 1024 gives each wave one
 super-step, so the prologue's issues and the first steps' waits are most of
 the kernel.  The inputs are random codes with finite scales, biases and x:
 the oracle checks of these kernels are in test_gpu_parity.py.
+
+The GEMMs get the same check over scale dtype x group size (which set the
+register-W GEMM's scale windows, unroll and compile-time wait counts): the
+register-W GEMM with K parts meeting in the workspace and on its persistent
+grid with a split last round, the split-K small-M GEMM (K parts, counters
+the last part returns to zero) and the LDS-dequant GEMM for the other code
+widths.
 """
 import numpy as np
 import pytest
@@ -40,27 +49,28 @@ def _values(rng, n, lo, hi, dtype):
     return (v.view(np.uint32) >> 16).astype(np.uint16)  # bf16 bits (truncated)
 
 
-def _repeat(ctx, M, K, N, gs, bits, xd, sbd, kernel, name, seed):
+def _repeat(ctx, M, K, N, gs, bits, xd, sbd, kernel, name, seed, od=F32, launches=LAUNCHES):
     from mlx_amd import abi, runtime
-    kern = abi.KERNEL_GEMM if kernel == "qgemm_small_kernel" else abi.KERNEL_GEMV
-    assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, F32, kern) == kernel, "case meant for " + kernel
+    kern = abi.KERNEL_GEMV if kernel.startswith("qgemv") else abi.KERNEL_GEMM
+    assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od, kern) == kernel, "case meant for " + kernel
     rng = np.random.default_rng(seed)
     x = _values(rng, M * K, -1.0, 1.0, xd)
     w_q = rng.integers(0, 2**32, N * K * bits // 32, dtype=np.uint32)
     s = _values(rng, N * (K // gs), 0.004, 0.02, sbd)
     b = _values(rng, N * (K // gs), -0.2, -0.05, sbd)
     ins = [ctx.upload(a) for a in (x, w_q, s, b)]
-    outs = [ctx.alloc(M * N * 4) for _ in range(LAUNCHES)]
+    outs = [ctx.alloc(M * N * runtime.esize(od)) for _ in range(launches)]
     try:
         print(f"[case] {name}", flush=True)
         for o in outs:
-            ctx.quantized_matmul(*ins, o, M, K, N, gs, bits, xd, sbd, F32, kern)
+            ctx.quantized_matmul(*ins, o, M, K, N, gs, bits, xd, sbd, od, kern)
         ctx.sync()
-        ys = [o.download(np.float32, (M, N)).view(np.uint32) for o in outs]
+        ys = [o.download(runtime.np_dtype(od), (M, N)) for o in outs]
     finally:
         for t in ins + outs:
             t.free()
-    assert np.isfinite(ys[0].view(np.float32)).all(), f"{name}: non-finite output"
+    assert np.isfinite(ys[0].astype(np.float32) if od != BF16 else
+                       (ys[0].astype(np.uint32) << 16).view(np.float32)).all(), f"{name}: non-finite output"
     bad = [i for i, y in enumerate(ys) if not np.array_equal(y, ys[0])]
     assert not bad, f"{name}: launches {bad} differ from launch 0"
 
@@ -89,3 +99,35 @@ def test_mid_gemv_rings_repeat(ctx, bits, sbd):
         for M, K in [(9, 1024), (16, 1024), (12, 4096)]:
             name = f"mid gemv b{bits} g{gs} sb{sbd} M{M} K{K}"
             _repeat(ctx, M, K, 4100, gs, bits, xd, sbd, "qgemv_mid_kernel", name, 9500 + 5 * bits + M + gs)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("sbd", SB, ids=["sb_f16", "sb_bf16", "sb_f32"])
+def test_rw_gemm_repeat(ctx, bits, sbd):
+    """qgemm_rw, every group size: 30 tiles in K parts meeting in the
+    workspace (M = 640, N = 1536, fp32 out), and 264 tiles on the persistent
+    grid, the last round's 8 tiles in K halves (M = 1024, N = 8448, 16-bit
+    out); K = 2048."""
+    xd = BF16 if sbd == BF16 else F16
+    for gs in GROUPS:
+        for M, N, od in [(640, 1536, F32), (1024, 8448, xd)]:
+            name = f"rw gemm b{bits} g{gs} sb{sbd} M{M} N{N}"
+            _repeat(ctx, M, 2048, N, gs, bits, xd, sbd, "qgemm_rw_kernel", name, 9700 + bits + M + gs, od=od,
+                    launches=12)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("sbd", SB, ids=["sb_f16", "sb_bf16", "sb_f32"])
+def test_split_k_and_lds_gemm_repeat(ctx, bits, sbd):
+    """qgemm_sk (M = 40, K = 3200: K % 1024 != 0, K parts) for every width,
+    and qgemm_kernel (M = 384, K = 1024, N = 1280) for the widths the
+    register-W GEMM does not take; every group size."""
+    from mlx_amd import abi
+    xd = BF16 if sbd == BF16 else F16
+    for gs in GROUPS:
+        _repeat(ctx, 40, 3200, 6000, gs, bits, xd, sbd, "qgemm_sk_kernel", f"split-K gemm b{bits} g{gs} sb{sbd}",
+                9800 + bits + gs, launches=12)
+        if bits in (4, 8) or ctx.kernel_name(384, 1024, 1280, gs, bits, xd, sbd, F32, abi.KERNEL_GEMM) is None:
+            continue  # 4/8-bit: the register-W GEMM; none: no GEMM form (6-bit, f32 scales, group 32)
+        _repeat(ctx, 384, 1024, 1280, gs, bits, xd, sbd, "qgemm_kernel", f"lds gemm b{bits} g{gs} sb{sbd}",
+                9900 + bits + gs, launches=12)
