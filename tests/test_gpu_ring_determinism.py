@@ -25,7 +25,7 @@ register-W GEMM's scale windows, unroll and compile-time wait counts): the
 register-W GEMM with K parts meeting in the workspace and on its persistent
 grid with a split last round, the split-K small-M GEMM (K parts, counters
 the last part returns to zero) and the LDS-dequant GEMM for the other code
-widths.
+widths.  So do the GEMV kernels AUTO picks for M = 1..8.
 """
 import numpy as np
 import pytest
@@ -50,9 +50,15 @@ def _values(rng, n, lo, hi, dtype):
 
 
 def _repeat(ctx, M, K, N, gs, bits, xd, sbd, kernel, name, seed, od=F32, launches=LAUNCHES):
+    """kernel: the kernel the case is meant for, or None for whatever AUTO
+    picks."""
     from mlx_amd import abi, runtime
-    kern = abi.KERNEL_GEMV if kernel.startswith("qgemv") else abi.KERNEL_GEMM
-    assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od, kern) == kernel, "case meant for " + kernel
+    if kernel is None:
+        kern = abi.KERNEL_AUTO
+        name += " (" + str(ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od, kern)) + ")"
+    else:
+        kern = abi.KERNEL_GEMV if kernel.startswith("qgemv") else abi.KERNEL_GEMM
+        assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od, kern) == kernel, "case meant for " + kernel
     rng = np.random.default_rng(seed)
     x = _values(rng, M * K, -1.0, 1.0, xd)
     w_q = rng.integers(0, 2**32, N * K * bits // 32, dtype=np.uint32)
@@ -131,3 +137,18 @@ def test_split_k_and_lds_gemm_repeat(ctx, bits, sbd):
             continue  # 4/8-bit: the register-W GEMM; none: no GEMM form (6-bit, f32 scales, group 32)
         _repeat(ctx, 384, 1024, 1280, gs, bits, xd, sbd, "qgemm_kernel", f"lds gemm b{bits} g{gs} sb{sbd}",
                 9900 + bits + gs, launches=12)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("sbd", SB, ids=["sb_f16", "sb_bf16", "sb_f32"])
+def test_gemv_repeat(ctx, bits, sbd):
+    """The GEMV kernels AUTO picks for M = 1..8 (whole-line, split-K,
+    decode, 4x4x4-MFMA, K-split whole-line, stream, skinny and row-run
+    kernels; several stage x or partial sums in LDS behind barriers), group
+    sizes 32 and 128, K = 4096 and 14336, ragged N = 4100."""
+    xd = BF16 if sbd == BF16 else F16
+    for gs in (32, 128):
+        for K in (4096, 14336):
+            for M in (1, 2, 3, 4, 6, 8):
+                _repeat(ctx, M, K, 4100, gs, bits, xd, sbd, None, f"gemv b{bits} g{gs} sb{sbd} M{M} K{K}",
+                        9600 + bits + gs + M + K, launches=12)
