@@ -5,7 +5,7 @@
 // helpers) by the per-bit-width translation units.
 //
 // A block is 4 waves, wave w owns R consecutive rows (R = 4, 6 or 7: see
-// line_rows below).  Every load is issued
+// line_rows7 and line_rows_narrow below).  Every load is issued
 // at the start, straight into registers:
 //   0. with R = 7 and the wave's own x: the first row's codes (below), so
 //      that the HBM stream is under way while steps 1-2 pass through the
