@@ -3,12 +3,15 @@
 // per load instruction.
 //
 // A block is KW waves and owns RB = 4 RG consecutive rows of W; wave w owns
-// codes 512 w .. 512 w + 511 of K (K = 512 KW).  Lane l = 4 b + j of a wave
-// is MFMA block b (b = l / 4) and column j (j = l % 4): for each 4-row group
-// of the block it loads the 32 codes 512 w + 32 b .. + 31 of the group's row
-// j with one 128-bit load.  So one wave load reads 4 rows x 16 lanes x 16
-// bytes, 256 contiguous bytes of each row, where the 16-row MFMA decode
-// kernel reads 64 and the whole-line kernels 512 or 1024.
+// CH chunks of 512 codes, codes 512 CH w .. 512 CH (w + 1) - 1 of K (K = 512
+// CH KW).  Lane l = 4 b + j of a wave is MFMA block b (b = l / 4) and column
+// j (j = l % 4): for each 4-row group of the block and each chunk h it loads
+// the 32 codes 512 (CH w + h) + 32 b .. + 31 of the group's row j with one
+// 128-bit load.  So one wave load reads 4 rows x 16 lanes x 16 bytes, 256
+// contiguous bytes of each row, where the 16-row MFMA decode kernel reads 64
+// and the whole-line kernels 512 or 1024.  CH = 2 lets K up to 16384 run on
+// at most 16 waves (long-K down projections at M <= 4); with CH = 1 the
+// kernel is the one-chunk form used up to K = 8192.
 //
 // MFMA: v_mfma_f32_4x4x4_16b_{f16,bf16} runs 16 independent 4x4x4 products,
 // block b on lanes 4 b .. 4 b + 3.  A = x (row i of block b on lane 4 b + i:
@@ -20,10 +23,12 @@
 //   D = sum v x = sx + sum q x / kPow over the lane's 32 codes,
 //   s sum q x + b sx = kPow (s D + (b / kPow - s) sx),
 // with sx = sum x over the lane's codes (of each row of the set: the lane's
-// own row i = j, the others from its quad by DPP).  The 16 blocks' values
-// are summed in registers (lane-half and row swaps, then row rotations by 4
-// and 8 lanes), parked in LDS, and after the last barrier thread t adds
-// the KW waves' parts of value t in wave order and stores kPow times it.
+// own row i = j, the others from its quad by DPP).  A lane's CH chunks each
+// get their own factors (their groups differ) and are added, and then the
+// 16 blocks' values are summed in registers (lane-half and row swaps, then
+// row rotations by 4 and 8 lanes), parked in LDS, and after the last
+// barrier thread t adds the KW waves' parts of value t in wave order and
+// stores kPow times it.
 //
 // Load order, as in the whole-line kernels: x and the block's scale rows
 // first (scale rows as 16-byte chunks over the block's threads), a block
@@ -72,7 +77,7 @@ struct Q4Lds {
 };
 
 // XS: sets of 4 rows of x (M <= 4 XS)
-template <int TX, int SB, int XS, int RG, int SBQ, int KW, bool EPI>
+template <int TX, int SB, int XS, int RG, int SBQ, int KW, bool EPI, int CH>
 __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
     const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int gshift, Epilogue ep) {
@@ -85,14 +90,14 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 3, blk = lane >> 2;
-    const uint32_t kc = (uint32_t)(wave * 512 + 32 * blk);  // the lane's first code
+    const uint32_t kc = (uint32_t)(wave * 512 * CH + 32 * blk);  // the lane's first code; chunk h at kc + 512 h
     const uint32_t row_bytes = (uint32_t)K / 2;
     const int G = K >> gshift;
     const int n0 = blockIdx.x * RB;
 
     // ---- 1. x: rows 4 s + j, the lane's 32 codes (rows past M re-read row
     // M - 1; they are never stored) ----
-    v4u32 xn[XS][4];
+    v4u32 xn[XS][CH][4];
     {
         const auto xr = buf_rsrc(x, (uint32_t)M * K * 2);
 #pragma unroll
@@ -100,7 +105,10 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
             const int m = 4 * s + j < M ? 4 * s + j : M - 1;
             const uint32_t off = ((uint32_t)m * K + kc) * 2u;
 #pragma unroll
-            for (int q = 0; q < 4; q++) xn[s][q] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * q, 0, 0);
+            for (int h = 0; h < CH; h++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    xn[s][h][q] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 1024u * h + 16 * q, 0, 0);
         }
     }
     // ---- 2. the block's scale and bias rows, from the 16-byte chunk holding
@@ -135,7 +143,7 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     __builtin_amdgcn_sched_barrier(0);
     // ---- 4. codes: row j of each 4-row group, 16 bytes per lane, groups in
     // order (rows past N re-read row N - 1, never stored) ----
-    v4u32 w[RG];
+    v4u32 w[RG][CH];
     {
         const size_t wleft = (size_t)(N - n0) * row_bytes;
         const auto wr = buf_rsrc(reinterpret_cast<const uint8_t*>(wq) + (size_t)n0 * row_bytes,
@@ -144,7 +152,9 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
         for (int rg = 0; rg < RG; rg++) {
             const int n = n0 + 4 * rg + j < N ? n0 + 4 * rg + j : N - 1;
             const uint32_t off = (uint32_t)(n - n0) * row_bytes + kc / 2;
-            w[rg] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, kCachePolicyNT);
+#pragma unroll
+            for (int h = 0; h < CH; h++)
+                w[rg][h] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 256u * h, 0, kCachePolicyNT);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -160,9 +170,10 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     }
     __syncthreads();
     // c0 multiplies D, c1 multiplies sx: s and b / kPow - s
-    float c0[RG], c1[RG];
-    {
-        const uint32_t g = kc >> gshift;
+    float c0[RG][CH], c1[RG][CH];
+#pragma unroll
+    for (int hh = 0; hh < CH; hh++) {
+        const uint32_t g = (kc + 512u * hh) >> gshift;
 #pragma unroll
         for (int rg = 0; rg < RG; rg++) {
             const uint32_t off = s_lead + ((uint32_t)(4 * rg + j) * G + g) * kSb;
@@ -174,33 +185,35 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
                 s = sb_value<SB>(*reinterpret_cast<const uint16_t*>(lds + L::kSb + off));
                 b = sb_value<SB>(*reinterpret_cast<const uint16_t*>(lds + L::kBi + off));
             }
-            c0[rg] = s;
-            c1[rg] = fmaf(b, 1.f / F::kPow, -s);
+            c0[rg][hh] = s;
+            c1[rg][hh] = fmaf(b, 1.f / F::kPow, -s);
         }
     }
 
     // ---- 6. x operands (the code operands' order) and sums of x: the
     // lane's own row 4 s + j, then rows 4 s + i from lane 4 b + i ----
-    v4u32 xo[XS][4];
-    float sxq[XS][4];
+    v4u32 xo[XS][CH][4];
+    float sxq[XS][CH][4];
     {
         const uint32_t one2 = TX == DT_F16 ? 0x3C003C00u : 0x3F803F80u;
 #pragma unroll
-        for (int s = 0; s < XS; s++) {
-            float sx = 0.f;
+        for (int s = 0; s < XS; s++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                xo[s][q] = skinny::x_operand<4, TX>(xn[s][q]);
-                sx = dot2(xn[s][q].x, one2, sx, TX);
-                sx = dot2(xn[s][q].y, one2, sx, TX);
-                sx = dot2(xn[s][q].z, one2, sx, TX);
-                sx = dot2(xn[s][q].w, one2, sx, TX);
+            for (int h = 0; h < CH; h++) {
+                float sx = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    xo[s][h][q] = skinny::x_operand<4, TX>(xn[s][h][q]);
+                    sx = dot2(xn[s][h][q].x, one2, sx, TX);
+                    sx = dot2(xn[s][h][q].y, one2, sx, TX);
+                    sx = dot2(xn[s][h][q].z, one2, sx, TX);
+                    sx = dot2(xn[s][h][q].w, one2, sx, TX);
+                }
+                sxq[s][h][0] = dpp_f<0x00>(sx);  // quad_perm [0,0,0,0]
+                sxq[s][h][1] = dpp_f<0x55>(sx);  // quad_perm [1,1,1,1]
+                sxq[s][h][2] = dpp_f<0xAA>(sx);  // quad_perm [2,2,2,2]
+                sxq[s][h][3] = dpp_f<0xFF>(sx);  // quad_perm [3,3,3,3]
             }
-            sxq[s][0] = dpp_f<0x00>(sx);  // quad_perm [0,0,0,0]
-            sxq[s][1] = dpp_f<0x55>(sx);  // quad_perm [1,1,1,1]
-            sxq[s][2] = dpp_f<0xAA>(sx);  // quad_perm [2,2,2,2]
-            sxq[s][3] = dpp_f<0xFF>(sx);  // quad_perm [3,3,3,3]
-        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -212,23 +225,33 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     asm volatile("" : "+v"(vm), "+v"(vmagic));
 #pragma unroll
     for (int rg = 0; rg < RG; rg++) {
-        v4u32 bop[4];
+        v4u32 bop[CH][4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const auto o = dec_code_operand<TX>(w[rg][q], vm, vmagic);
-            bop[q] = v4u32{o.x, o.y, o.z, o.w};
-        }
-#pragma unroll
-        for (int s = 0; s < XS; s++) {
-            f4 d = {0.f, 0.f, 0.f, 0.f};
+        for (int h = 0; h < CH; h++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                d = mfma4<TX>(xo[s][q].x, xo[s][q].y, bop[q].x, bop[q].y, d);
-                d = mfma4<TX>(xo[s][q].z, xo[s][q].w, bop[q].z, bop[q].w, d);
+                const auto o = dec_code_operand<TX>(w[rg][h][q], vm, vmagic);
+                bop[h][q] = v4u32{o.x, o.y, o.z, o.w};
+            }
+#pragma unroll
+        for (int s = 0; s < XS; s++) {
+            f4 d[CH];
+#pragma unroll
+            for (int h = 0; h < CH; h++) {
+                d[h] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    d[h] = mfma4<TX>(xo[s][h][q].x, xo[s][h][q].y, bop[h][q].x, bop[h][q].y, d[h]);
+                    d[h] = mfma4<TX>(xo[s][h][q].z, xo[s][h][q].w, bop[h][q].z, bop[h][q].w, d[h]);
+                }
             }
             float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = fmaf(c0[rg], d[i], c1[rg] * sxq[s][i]);
+            for (int i = 0; i < 4; i++) {
+                v[i] = fmaf(c0[rg][0], d[0][i], c1[rg][0] * sxq[s][0][i]);
+#pragma unroll
+                for (int h = 1; h < CH; h++) v[i] += fmaf(c0[rg][h], d[h][i], c1[rg][h] * sxq[s][h][i]);
+            }
             // the 4 rows of 16 lanes (lane-half and row swaps: row r then
             // holds value pi(r)), then the 4 quads of each row
             float z = swap16_sum(swap32_sum(v[0], v[1]), swap32_sum(v[2], v[3]));
@@ -257,7 +280,7 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
 
 // Rows per block: 28 where that spreads the blocks over the 256 CUs more
 // evenly than 16 (as the K-split whole-line kernel)
-template <int TX, int SB, int XS, int RG, int SBQ, int KW>
+template <int TX, int SB, int XS, int RG, int SBQ, int KW, int CH>
 LuxStatus launch_k(const QmmArgs& a, hipStream_t st) {
     using L = Q4Lds<RG, XS, SBQ, KW>;
     static_assert(L::kBytes <= 160 * 1024, "LDS");
@@ -265,19 +288,19 @@ LuxStatus launch_k(const QmmArgs& a, hipStream_t st) {
     if constexpr (L::kBytes > 64 * 1024) {
         // once per instantiation (a function-local static initializes once)
         static const hipError_t attr[2] = {
-            hipFuncSetAttribute(reinterpret_cast<const void*>(qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, true>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, true, CH>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes),
-            hipFuncSetAttribute(reinterpret_cast<const void*>(qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, false>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, false, CH>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes)};
         if (attr[0] != hipSuccess || attr[1] != hipSuccess) return LuxStatus::Internal;
     }
     const int gshift = a.group_size == 32 ? 5 : a.group_size == 64 ? 6 : 7;
     const int blocks = (a.N + 4 * RG - 1) / (4 * RG);
     if (a.has_epilogue())
-        hipLaunchKernelGGL((qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, true>), dim3(blocks), dim3(64 * KW), L::kBytes,
+        hipLaunchKernelGGL((qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, true, CH>), dim3(blocks), dim3(64 * KW), L::kBytes,
                            st, a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K, a.N, gshift, a.epi());
     else
-        hipLaunchKernelGGL((qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, false>), dim3(blocks), dim3(64 * KW), L::kBytes,
+        hipLaunchKernelGGL((qgemv_q4_kernel<TX, SB, XS, RG, SBQ, KW, false, CH>), dim3(blocks), dim3(64 * KW), L::kBytes,
                            st, a.x, a.wq, a.scales, a.biases, a.y, a.M, a.K, a.N, gshift, a.epi());
     return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
 }

@@ -91,6 +91,23 @@ def test_quantize_bit_exact(ctx, oracle, bits, gs):
 
 # ---- GEMV ---------------------------------------------------------------
 
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_q4_two_chunk_parity(ctx, oracle, xd, sbd, od):
+    """4-bit codes, M = 2..4 at K = 12288 / 14336 / 16384: the 4x4x4-MFMA
+    decode kernel with two 512-code chunks per lane on K / 1024 waves (each
+    chunk with its own group factors), 16-row blocks with a ragged last one,
+    every group size."""
+    O = oracle
+    for i, (K, N, gs) in enumerate([(12288, 300, 64), (14336, 77, 32), (16384, 130, 128), (14336, 4100, 64),
+                                    (12288, 33, 32), (16384, 60, 64)]):
+        M = 2 + i % 3
+        assert ctx.kernel_name(M, K, N, gs, 4, xd, sbd, od) == "qgemv_q4_kernel"
+        x, w_q, s, b, _ = O.make_problem(M, K, N, 4, gs, xd, sbd, seed=7300 + M + K + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od)
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, 4, xd, sbd, od)
+        check_output(O, y, want, od, f"q4 two chunks M{M} K{K} N{N} g{gs}")
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_line_gemv_six_rows(ctx, oracle, bits, xd, sbd, od):
@@ -259,7 +276,9 @@ def test_kline_gemv_long_k(ctx, oracle, bits, xd, sbd, od):
     whole-line kernel with 8 waves per block (4096 < K <= 8192, where it takes
     M = 2 and 2-bit codes) and 16 (K <= 16384, every M), each wave's part
     under a whole wave (K = 6144: 768 codes, 48 lanes), every group size, f32
-    scales whose block rows take two LDS passes (K = 16384, g32), ragged N."""
+    scales whose block rows take two LDS passes (K = 16384, g32), ragged N;
+    4-bit codes at K = 12288 / 14336 / 16384 run the 4x4x4-MFMA decode kernel
+    with two chunks per lane instead."""
     O = oracle
     for i, (K, N, gs) in enumerate([(6144, 100, 64), (8192, 33, 32), (14336, 70, 32), (16384, 40, 128),
                                     (16384, 18, 32), (12288, 50, 64)]):
@@ -751,6 +770,7 @@ FUSED_CASES = [
     (1, 4096, 300, 4, 64, F16),     # whole-line GEMV
     (1, 4096, 5120, 3, 64, BF16),   # whole-line GEMV, 6-row waves
     (1, 14336, 70, 4, 64, BF16),    # split-K GEMV
+    (3, 14336, 72, 4, 64, F16),     # 4x4x4-MFMA decode, two chunks per lane
     (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
     (2, 4096, 40, 3, 64, F16),      # stream GEMV (two rows of x, 3-bit)
     (6, 960, 70, 3, 64, F16),       # row-run GEMV (3-bit, K % 1024 != 0)
