@@ -59,9 +59,10 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     // / 4 / 6 / 8 8.8 / 9.1 / 9.0 / 11.7 / 12.1 against 10.2 / 12.1 / 12.2 /
     // 12.6 / 13.0; K = N = 8192 M = 4 12.2 against 13.8 (M = 8 20.1 against
     // 15.0); K = 2048, N = 8192, M = 8 5.6 against 5.4.  At M <= 4 it also
-    // takes K = 12288 / 14336 / 16384 (two chunks per lane) from the K-split
+    // takes 8192 < K <= 16384 (two chunks per lane) from the K-split
     // whole-line kernel: K = 14336, N = 4096, M = 2 / 3 / 4 9.9 / 10.5 / 11.2
-    // against 11.9 / 16.1 / 16.2 (qgemv_q4.hip)
+    // against 11.9 / 16.1 / 16.2; K = 11008 8.6 / 9.0 / 9.5 against 11.2 /
+    // 15.6 / 15.6 (qgemv_q4.hip)
     if (args.M >= 2 && args.bits == 4 && (args.M <= 4 || (args.M <= 8 && args.K == 4096))) {
         const LuxStatus s = launch_qgemv_q4(args, st);
         if (s != LuxStatus::NotSupported) return s;

@@ -4,7 +4,7 @@
 //
 // A block is KW waves and owns RB = 4 RG consecutive rows of W; wave w owns
 // CH chunks of 512 codes, codes 512 CH w .. 512 CH (w + 1) - 1 of K (K = 512
-// CH KW).  Lane l = 4 b + j of a wave is MFMA block b (b = l / 4) and column
+// CH KW with one chunk; with two, K <= 1024 KW and codes past K idle).  Lane l = 4 b + j of a wave is MFMA block b (b = l / 4) and column
 // j (j = l % 4): for each 4-row group of the block and each chunk h it loads
 // the 32 codes 512 (CH w + h) + 32 b .. + 31 of the group's row j with one
 // 128-bit load.  So one wave load reads 4 rows x 16 lanes x 16 bytes, 256
@@ -94,6 +94,12 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     const uint32_t row_bytes = (uint32_t)K / 2;
     const int G = K >> gshift;
     const int n0 = blockIdx.x * RB;
+    // with two chunks, K need not fill the waves (part of a chunk, a whole
+    // chunk or whole waves idle): a lane's 32-code block past K (K % 32 =
+    // 0) loads no x and no codes and gets zero factors, so it adds exactly 0
+    bool in_k[CH];
+#pragma unroll
+    for (int h = 0; h < CH; h++) in_k[h] = CH == 1 || kc + 512u * h < (uint32_t)K;
 
     // ---- 1. x: rows 4 s + j, the lane's 32 codes (rows past M re-read row
     // M - 1; they are never stored) ----
@@ -108,7 +114,8 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
             for (int h = 0; h < CH; h++)
 #pragma unroll
                 for (int q = 0; q < 4; q++)
-                    xn[s][h][q] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 1024u * h + 16 * q, 0, 0);
+                    xn[s][h][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                        xr, in_k[h] ? off + 1024u * h + 16 * q : kZeroOff, 0, 0);
         }
     }
     // ---- 2. the block's scale and bias rows, from the 16-byte chunk holding
@@ -154,7 +161,8 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
             const uint32_t off = (uint32_t)(n - n0) * row_bytes + kc / 2;
 #pragma unroll
             for (int h = 0; h < CH; h++)
-                w[rg][h] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 256u * h, 0, kCachePolicyNT);
+                w[rg][h] = __builtin_amdgcn_raw_buffer_load_b128(wr, in_k[h] ? off + 256u * h : kZeroOff, 0,
+                                                                 kCachePolicyNT);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -173,7 +181,7 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
     float c0[RG][CH], c1[RG][CH];
 #pragma unroll
     for (int hh = 0; hh < CH; hh++) {
-        const uint32_t g = (kc + 512u * hh) >> gshift;
+        const uint32_t g = in_k[hh] ? (kc + 512u * hh) >> gshift : 0u;
 #pragma unroll
         for (int rg = 0; rg < RG; rg++) {
             const uint32_t off = s_lead + ((uint32_t)(4 * rg + j) * G + g) * kSb;
@@ -185,8 +193,8 @@ __global__ __launch_bounds__(64 * KW) void qgemv_q4_kernel(
                 s = sb_value<SB>(*reinterpret_cast<const uint16_t*>(lds + L::kSb + off));
                 b = sb_value<SB>(*reinterpret_cast<const uint16_t*>(lds + L::kBi + off));
             }
-            c0[rg][hh] = s;
-            c1[rg][hh] = fmaf(b, 1.f / F::kPow, -s);
+            c0[rg][hh] = in_k[hh] ? s : 0.f;
+            c1[rg][hh] = in_k[hh] ? fmaf(b, 1.f / F::kPow, -s) : 0.f;
         }
     }
 

@@ -93,13 +93,18 @@ def test_quantize_bit_exact(ctx, oracle, bits, gs):
 
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_q4_two_chunk_parity(ctx, oracle, xd, sbd, od):
-    """4-bit codes, M = 2..4 at K = 12288 / 14336 / 16384: the 4x4x4-MFMA
-    decode kernel with two 512-code chunks per lane on K / 1024 waves (each
-    chunk with its own group factors), 16-row blocks with a ragged last one,
-    every group size."""
+    """4-bit codes, M = 2..4, 8192 < K <= 16384: the 4x4x4-MFMA
+    decode kernel with two 512-code chunks per lane on 12, 14 or 16 waves
+    (each chunk with its own group factors), 16-row blocks with a ragged
+    last one, every group size; K below the waves' reach leaves lanes past K
+    idle: half of the last chunk's lanes (K = 11008), a whole last chunk (K
+    = 13824), whole waves (K = 9216), all of waves 8..11 but two 32-code
+    blocks of wave 8's first chunk (K = 8256)."""
     O = oracle
     for i, (K, N, gs) in enumerate([(12288, 300, 64), (14336, 77, 32), (16384, 130, 128), (14336, 4100, 64),
-                                    (12288, 33, 32), (16384, 60, 64)]):
+                                    (12288, 33, 32), (16384, 60, 64), (11008, 301, 64), (13824, 70, 128),
+                                    (9216, 45, 32), (11008, 96, 32), (10240, 20, 128), (15360, 50, 64),
+                                    (8256, 40, 32)]):
         M = 2 + i % 3
         assert ctx.kernel_name(M, K, N, gs, 4, xd, sbd, od) == "qgemv_q4_kernel"
         x, w_q, s, b, _ = O.make_problem(M, K, N, 4, gs, xd, sbd, seed=7300 + M + K + N)
