@@ -34,6 +34,15 @@ static LuxStatus launch_mx_bits(const QmmArgs& a, hipStream_t st) {
 // fits in 64 KB of LDS (two blocks per CU).
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
+    // rows m0 .. m0 + mc - 1 of x and y
+    auto rows = [&](int m0, int mc) {
+        QmmArgs a = args;
+        a.M = mc;
+        const size_t xel = args.x_dtype == DT_F32 ? 4 : 2, yel = args.out_dtype == DT_F32 ? 4 : 2;
+        a.x = static_cast<const uint8_t*>(args.x) + (size_t)m0 * args.K * xel;
+        a.y = static_cast<uint8_t*>(args.y) + (size_t)m0 * args.N * yel;
+        return a;
+    };
     // 2..16 rows of x: the MFMA kernels where they apply (16-bit x; the
     // decode kernel takes 4-bit codes and M <= 8, the LDS-ring kernel 4/8-bit
     // codes; both need K % 1024 == 0), except where the stream kernel (M <= 4,
@@ -67,6 +76,24 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const LuxStatus s = launch_qgemv_q4(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
+    // 5..8 rows of x, 16-bit x, 8192 < K <= 16384: rows 0..3 and the rest as
+    // two launches of the kernels above (the second finds W in the Infinity
+    // Cache) where the LDS-ring kernel does not take the shape (K % 1024 !=
+    // 0, 2-bit codes) or fills half the CUs (4-bit, N <= 4096; its 32-row
+    // blocks).  Same box, g64, N = 4096, M = 5 / 6 / 8, us per launch: K =
+    // 11008, 4-bit 32.3 / 35.5 / 46.8 -> 18.5 / 17.5 / 18.7 (split-K kernel
+    // before), 8-bit 37.8 / 41.1 / 54.1 -> 32.1 / 34.7 / 39.3; K = 14336,
+    // 2-bit 34.4 / 41.0 / 54.4 -> 23.1 / 25.0 / 29.5, 4-bit 25.4 / 25.5 /
+    // 25.4 -> 21.2 / 21.5 / 23.0 (LDS-ring kernel before).  Not taken: 8-bit
+    // at K = 14336 (27.4 -> 33.9..40.7) and 4-bit at N = 8192 (27.5 ->
+    // 37.8..44.9), where the LDS-ring kernel fills the CUs.
+    if (args.M >= 5 && args.M <= 8 && args.x_dtype != DT_F32 && args.K > 8192 && args.K <= 16384 &&
+        (args.bits == 2 || args.bits == 4 || args.bits == 8) &&
+        (args.K % 1024 != 0 || args.bits == 2 || (args.bits == 4 && args.N <= 4096))) {
+        const LuxStatus s = launch_qgemv(rows(0, 4), st);
+        if (s != LuxStatus::Ok) return s;
+        return launch_qgemv(rows(4, args.M - 4), st);
+    }
     if (args.M >= 2 && args.M <= 4) {
         const LuxStatus s = launch_mx_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;
@@ -92,15 +119,6 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const LuxStatus s = launch_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
-    // rows m0 .. m0 + mc - 1 of x and y
-    auto rows = [&](int m0, int mc) {
-        QmmArgs a = args;
-        a.M = mc;
-        const size_t xel = args.x_dtype == DT_F32 ? 4 : 2, yel = args.out_dtype == DT_F32 ? 4 : 2;
-        a.x = static_cast<const uint8_t*>(args.x) + (size_t)m0 * args.K * xel;
-        a.y = static_cast<uint8_t*>(args.y) + (size_t)m0 * args.N * yel;
-        return a;
-    };
     // f32 x with more than 4 rows: chunks of 4 (a last single row on the
     // M = 1 kernels) on the K-split whole-line kernel where it applies
     // (M = 8, K = 4096, N = 14336, 4-bit: the row-run kernel took 126.9 us)

@@ -113,6 +113,25 @@ def test_q4_two_chunk_parity(ctx, oracle, xd, sbd, od):
         check_output(O, y, want, od, f"q4 two chunks M{M} K{K} N{N} g{gs}")
 
 
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_row_split_long_k_parity(ctx, oracle, xd, sbd, od):
+    """M = 5..8, 8192 < K <= 16384 where the LDS-ring kernel does not take
+    the shape (K % 1024 != 0, 2-bit codes) or fills half the CUs (4-bit, N
+    <= 4096): rows 0..3 and the rest of x as two launches of the M <= 4
+    kernels (the two-chunk decode kernel for 4-bit codes, the K-split
+    whole-line kernel for 2 and 8; a fifth row on the M = 1 kernels), each
+    writing its own rows of y."""
+    O = oracle
+    for (M, K, N, bits, gs) in [(5, 11008, 301, 4, 64), (6, 14336, 200, 4, 32), (8, 11008, 96, 8, 32),
+                                (7, 14336, 130, 2, 128), (5, 9216, 64, 2, 32), (8, 13824, 77, 4, 128),
+                                (6, 10752, 45, 8, 64)]:
+        assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od) in ("qgemv_q4_kernel", "qgemv_mx_kernel")
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=7600 + M + K + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"row split M{M} K{K} N{N} b{bits} g{gs}")
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_line_gemv_six_rows(ctx, oracle, bits, xd, sbd, od):
@@ -776,6 +795,7 @@ FUSED_CASES = [
     (1, 4096, 5120, 3, 64, BF16),   # whole-line GEMV, 6-row waves
     (1, 14336, 70, 4, 64, BF16),    # split-K GEMV
     (3, 14336, 72, 4, 64, F16),     # 4x4x4-MFMA decode, two chunks per lane
+    (6, 11008, 72, 4, 64, BF16),    # rows 0..3 and 4..5 as two launches (two-chunk decode)
     (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
     (2, 4096, 40, 3, 64, F16),      # stream GEMV (two rows of x, 3-bit)
     (6, 960, 70, 3, 64, F16),       # row-run GEMV (3-bit, K % 1024 != 0)
