@@ -196,7 +196,7 @@ def test_every_kernel_family_is_chosen_somewhere():
         "qgemv_line_kernel": (1, 4096, 14336, 64, 4, F16),       # M = 1, K up to 16384
         "qgemv_split_kernel": (1, 14336, 4096, 64, 4, F16),      # M = 1 down projections, K > 8192
         "qgemv_stream_kernel": (2, 4096, 14336, 64, 3, F16),     # M = 2..8, 3/5/6-bit codes
-        "qgemv_kernel": (4, 4096, 11008, 64, 3, F32),            # f32 x, 3/5/6-bit codes, M >= 2
+        "qgemv_kernel": (16, 4096, 11008, 64, 3, F32),           # f32 x, 3/5/6-bit codes, M > 8
         "qgemv_mx_kernel": (4, 4096, 14336, 64, 8, F16),         # M = 2..4, 8-bit codes
         "qgemv_q4_kernel": (4, 4096, 14336, 64, 4, F16),         # M = 2..8, 4-bit codes, K = 4096
         "qgemv_dec_kernel": (6, 8192, 8192, 64, 4, F16),         # M = 5..8, 4-bit codes, K = 8192

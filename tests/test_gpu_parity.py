@@ -132,6 +132,23 @@ def test_row_split_long_k_parity(ctx, oracle, xd, sbd, od):
         check_output(O, y, want, od, f"row split M{M} K{K} N{N} b{bits} g{gs}")
 
 
+@pytest.mark.parametrize("sbd,od", [(F32, F32), (F16, F32), (BF16, F16), (F32, BF16)])
+def test_f32_x_per_row_parity(ctx, oracle, sbd, od):
+    """f32 x with 3/5/6-bit codes, M = 2..8, K <= 4096: one launch of the
+    M = 1 kernels per row of x (whole-line for 3/6-bit, stream for 5-bit),
+    each writing its own row of y; ragged N, every group size, K = 960 (an
+    odd chunk count)."""
+    O = oracle
+    for (M, K, N, bits, gs) in [(2, 4096, 300, 3, 64), (3, 2048, 130, 5, 32), (4, 4096, 77, 6, 128),
+                                (8, 1024, 96, 3, 32), (5, 4096, 40, 5, 64), (7, 960, 33, 6, 64),
+                                (6, 4096, 1030, 6, 32)]:
+        assert ctx.kernel_name(M, K, N, gs, bits, F32, sbd, od) in ("qgemv_line_kernel", "qgemv_stream_kernel")
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, F32, sbd, seed=7700 + M + K + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, F32, sbd, od)
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, F32, sbd, od)
+        check_output(O, y, want, od, f"f32 x per row M{M} K{K} N{N} b{bits} g{gs}")
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_line_gemv_six_rows(ctx, oracle, bits, xd, sbd, od):
@@ -799,6 +816,7 @@ FUSED_CASES = [
     (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
     (2, 4096, 40, 3, 64, F16),      # stream GEMV (two rows of x, 3-bit)
     (6, 960, 70, 3, 64, F16),       # row-run GEMV (3-bit, K % 1024 != 0)
+    (3, 1024, 50, 6, 64, F32),      # whole-line GEMV once per row (f32 x, 6-bit)
     (6, 512, 96, 4, 64, BF16),      # skinny MFMA GEMV
     (3, 1024, 72, 8, 128, BF16),    # K-split whole-line GEMV (three rows of x, 8-bit)
     (6, 4096, 64, 4, 64, BF16),     # decode MFMA kernel
