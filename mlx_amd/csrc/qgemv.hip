@@ -146,6 +146,22 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
             if (m0 + 4 >= args.M) return LuxStatus::Ok;
         }
     }
+    // 16-bit x, K > 4096, three rows or more that no kernel above took:
+    // pairs of rows on the split-K kernel (a last single row on the M = 1
+    // kernels) rather than the row-run kernel in chunks of up to 4 rows, or
+    // the generic kernel where one row of x overflows its 64 KB staging.
+    // Same box, g64, us per launch: K = 5120, N = 13824, 3-bit, M = 3 / 4 /
+    // 8: 81.8 / 99.5 / 186.7 -> 36.3 / 41.8 / 82.6 (5/6-bit alike); K =
+    // 6144, N = 4096, M = 4: 36.0 -> 16.3; 4-bit K = 6656 40.6 -> 15.8; K =
+    // 28672, N = 8192, 3-bit M = 3 / 8: 17132 / 24198 -> 92.7 / 238.5
+    if (args.x_dtype != DT_F32 && args.K > 4096 && args.M > 2) {
+        for (int m0 = 0; m0 < args.M; m0 += 2) {
+            const LuxStatus s = launch_bits(rows(m0, args.M - m0 < 2 ? 1 : 2), st);
+            if (m0 == 0 && s == LuxStatus::NotSupported) break;  // nothing launched: the chunks below
+            if (s != LuxStatus::Ok) return s;
+            if (m0 + 2 >= args.M) return LuxStatus::Ok;
+        }
+    }
     // (f32 x: at most 4 rows, the row-run kernel's registers at 8 do not fit)
     int chunk = args.x_dtype == DT_F32 ? 4 : 8;
     while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;

@@ -132,6 +132,24 @@ def test_row_split_long_k_parity(ctx, oracle, xd, sbd, od):
         check_output(O, y, want, od, f"row split M{M} K{K} N{N} b{bits} g{gs}")
 
 
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_split_k_row_pairs_parity(ctx, oracle, xd, sbd, od):
+    """16-bit x, K > 4096, M = 3..8 where no M-wide kernel takes the shape
+    (3/5/6-bit codes; K % 1024 != 0 for 4/8-bit; K beyond the row-run
+    kernel's x staging): pairs of rows on the split-K kernel, a last single
+    row on the M = 1 split-K kernel, each launch writing its own rows of y;
+    K up to 32768, ragged N, every group size."""
+    O = oracle
+    for (M, K, N, bits, gs) in [(3, 5120, 130, 3, 64), (4, 6144, 77, 5, 32), (5, 28672, 40, 6, 128),
+                                (8, 4160, 33, 8, 64), (7, 6656, 50, 4, 128), (6, 32768, 20, 2, 64),
+                                (3, 28672, 64, 3, 64)]:
+        assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od) == "qgemv_split_kernel"
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=7800 + M + K + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"split-K row pairs M{M} K{K} N{N} b{bits} g{gs}")
+
+
 @pytest.mark.parametrize("sbd,od", [(F32, F32), (F16, F32), (BF16, F16), (F32, BF16)])
 def test_f32_x_per_row_parity(ctx, oracle, sbd, od):
     """f32 x with 3/5/6-bit codes, M = 2..8, K <= 4096: one launch of the
@@ -811,6 +829,7 @@ FUSED_CASES = [
     (1, 4096, 300, 4, 64, F16),     # whole-line GEMV
     (1, 4096, 5120, 3, 64, BF16),   # whole-line GEMV, 6-row waves
     (1, 14336, 70, 4, 64, BF16),    # split-K GEMV
+    (3, 5120, 40, 5, 64, BF16),     # split-K GEMV on pairs of rows (5-bit, three rows of x)
     (3, 14336, 72, 4, 64, F16),     # 4x4x4-MFMA decode, two chunks per lane
     (6, 11008, 72, 4, 64, BF16),    # rows 0..3 and 4..5 as two launches (two-chunk decode)
     (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
