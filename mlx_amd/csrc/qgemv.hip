@@ -162,8 +162,12 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
             if (m0 + 2 >= args.M) return LuxStatus::Ok;
         }
     }
-    // (f32 x: at most 4 rows, the row-run kernel's registers at 8 do not fit)
-    int chunk = args.x_dtype == DT_F32 ? 4 : 8;
+    // (f32 x: at most 4 rows, the row-run kernel's registers at 8 do not fit;
+    // 16-bit x at K <= 4096: 4 rows, so that the chunks run on the stream
+    // kernel, not the row-run kernel.  Same box, g64, us per launch, M = 8,
+    // K = 2048, N = 8192: 3-bit 55.9 -> 16.2, 2-bit 56.0 -> 15.4; M = 6, K =
+    // 3072, N = 14336, 5-bit 83.9 -> 26.0; 8-bit N = 8192 60.7 -> 14.9)
+    int chunk = args.x_dtype == DT_F32 || args.K <= 4096 ? 4 : 8;
     while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
     // one row of x may still run on the split-K stream kernel (K <= 32768),
     // which stages x in up to 160 KB; the row-run kernel declines it itself

@@ -150,6 +150,21 @@ def test_split_k_row_pairs_parity(ctx, oracle, xd, sbd, od):
         check_output(O, y, want, od, f"split-K row pairs M{M} K{K} N{N} b{bits} g{gs}")
 
 
+@pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
+def test_stream_row_chunks_parity(ctx, oracle, xd, sbd, od):
+    """16-bit x, K <= 4096, M = 5..8 where no M-wide kernel takes the shape:
+    chunks of 4 rows on the stream kernel (the last chunk 1..4 rows), each
+    launch writing its own rows of y; ragged N, every group size."""
+    O = oracle
+    for (M, K, N, bits, gs) in [(5, 2048, 130, 3, 64), (8, 1024, 77, 6, 32), (6, 3072, 40, 5, 128),
+                                (8, 2560, 33, 4, 64), (7, 512, 64, 2, 32), (6, 1536, 50, 8, 128)]:
+        assert ctx.kernel_name(M, K, N, gs, bits, xd, sbd, od) == "qgemv_stream_kernel"
+        x, w_q, s, b, _ = O.make_problem(M, K, N, bits, gs, xd, sbd, seed=7900 + M + K + N)
+        y = run(ctx, x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        want = O.quantized_matmul(x, w_q, s, b, M, K, N, gs, bits, xd, sbd, od)
+        check_output(O, y, want, od, f"stream row chunks M{M} K{K} N{N} b{bits} g{gs}")
+
+
 @pytest.mark.parametrize("sbd,od", [(F32, F32), (F16, F32), (BF16, F16), (F32, BF16)])
 def test_f32_x_per_row_parity(ctx, oracle, sbd, od):
     """f32 x with 3/5/6-bit codes, M = 2..8, K <= 4096: one launch of the
