@@ -4,11 +4,6 @@
 namespace lxq {
 using namespace gemv;
 
-size_t gemv_lds_bytes(int MR, int K, int x_dtype) {
-    const size_t elem = x_dtype == DT_F32 ? 4 : 2, stride = x_dtype == DT_F32 ? 68 : 72;
-    return (size_t)MR * (K / 64) * stride * elem + (size_t)MR * (K / 32) * 4;
-}
-
 static LuxStatus launch_bits(const QmmArgs& a, hipStream_t st) {
     switch (a.bits) {
     case 2: return launch_b<2>(a, st);
@@ -30,8 +25,10 @@ static LuxStatus launch_mx_bits(const QmmArgs& a, hipStream_t st) {
     }
 }
 
-// M is processed in chunks of up to 8 rows of x, as many as the staged x
-// fits in 64 KB of LDS (two blocks per CU).
+// Rows of x that no kernel takes whole are split over launches: four rows
+// of 16-bit x per launch of the stream kernel (K <= 4096), two per launch of
+// the split-K kernel (K > 4096), one row of f32 x per launch of the M = 1
+// kernels.  NotSupported: the generic kernel.
 LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
     if (args.K % 64 != 0) return LuxStatus::NotSupported;
     // rows m0 .. m0 + mc - 1 of x and y
@@ -112,24 +109,31 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         const LuxStatus s = launch_qmm_skinny(args, st);
         if (s != LuxStatus::NotSupported) return s;
     }
-    // f32 x with 3/5/6-bit codes (no K-split whole-line form), 2..8 rows, K <=
-    // 4096: one launch of the M = 1 kernels per row (whole-line; stream for
-    // 5-bit) instead of the row-run kernel.  Same box, g64, f32 x, scales and
-    // output, us per launch, K = 4096, N = 14336, M = 2 / 3 / 4 / 8: 3-bit
-    // 35.6 / 45.6 / 68.3 / 133.4 -> 17.6 / 26.0 / 34.5 / 68.0; 5-bit 56.5 /
-    // 72.0 / 114.9 / 224.2 -> 22.1 / 32.8 / 43.3 / 86.0; 6-bit 57.0 / 70.2 /
-    // 116.4 / 227.5 -> 23.4 / 34.4 / 45.8 / 88.8 (N = 4096: 40-52 % less)
-    if (args.x_dtype == DT_F32 && args.M >= 2 && args.M <= 8 && args.K <= 4096 &&
-        (args.bits == 3 || args.bits == 5 || args.bits == 6)) {
+    // f32 x, two rows or more, where the K-split whole-line kernel does not
+    // run (3/5/6-bit codes; K > 16384; K not a whole number of its waves'
+    // 16-code steps, launch_mx_b): one launch of the M = 1 kernels per
+    // row (whole-line or stream up to K = 4096, split-K up to 32768) instead
+    // of the row-run kernel (since retired), or the generic kernel where one
+    // row of f32 x overflowed that kernel's staging (K >= 18944).  Same box, g64,
+    // f32 x, scales and output, us per launch, K = 4096, N = 14336, M = 2 /
+    // 3 / 4 / 8: 3-bit 35.6 / 45.6 / 68.3 / 133.4 -> 17.6 / 26.0 / 34.5 /
+    // 68.0; 5-bit 56.5 / 72.0 / 114.9 / 224.2 -> 22.1 / 32.8 / 43.3 / 86.0;
+    // 6-bit 57.0 / 70.2 / 116.4 / 227.5 -> 23.4 / 34.4 / 45.8 / 88.8 (N =
+    // 4096: 40-52 % less).  Every row is the same launch, so the gain holds
+    // at any M.
+    if (args.x_dtype == DT_F32 && args.M >= 2 &&
+        (args.bits == 3 || args.bits == 5 || args.bits == 6 || args.K > 16384 ||
+         args.K % (16 * (args.K > 8192 ? 16 : args.K > 4096 ? 8 : 4)) != 0)) {
         for (int m0 = 0; m0 < args.M; m0++) {
             const LuxStatus s = launch_bits(rows(m0, 1), st);
+            if (m0 == 0 && s == LuxStatus::NotSupported) break;  // nothing launched: the kernels below
             if (s != LuxStatus::Ok) return s;
+            if (m0 + 1 == args.M) return LuxStatus::Ok;
         }
-        return LuxStatus::Ok;
     }
     // one or two rows of x: the whole-line, stream and split-K kernels take
     // them whole (the split-K kernel stages both x rows itself, up to
-    // K = 16384); only if they decline, the chunked row-run kernel below
+    // K = 16384); only if they decline, the row chunks below
     if (args.M <= 2) {
         const LuxStatus s = launch_bits(args, st);
         if (s != LuxStatus::NotSupported) return s;
@@ -141,14 +145,14 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
         for (int m0 = 0; m0 < args.M; m0 += 4) {
             const QmmArgs a = rows(m0, args.M - m0 < 4 ? args.M - m0 : 4);
             const LuxStatus s = a.M >= 2 ? launch_mx_bits(a, st) : launch_bits(a, st);
-            if (m0 == 0 && s == LuxStatus::NotSupported) break;  // nothing launched: the row-run kernel below
+            if (m0 == 0 && s == LuxStatus::NotSupported) break;  // nothing launched: the row chunks below
             if (s != LuxStatus::Ok) return s;
             if (m0 + 4 >= args.M) return LuxStatus::Ok;
         }
     }
     // 16-bit x, K > 4096, three rows or more that no kernel above took:
     // pairs of rows on the split-K kernel (a last single row on the M = 1
-    // kernels) rather than the row-run kernel in chunks of up to 4 rows, or
+    // kernels) rather than a row-run kernel (since retired) in chunks of up to 4 rows, or
     // the generic kernel where one row of x overflows its 64 KB staging.
     // Same box, g64, us per launch: K = 5120, N = 13824, 3-bit, M = 3 / 4 /
     // 8: 81.8 / 99.5 / 186.7 -> 36.3 / 41.8 / 82.6 (5/6-bit alike); K =
@@ -162,18 +166,15 @@ LuxStatus launch_qgemv(const QmmArgs& args, hipStream_t st) {
             if (m0 + 2 >= args.M) return LuxStatus::Ok;
         }
     }
-    // (f32 x: at most 4 rows, the row-run kernel's registers at 8 do not fit;
-    // 16-bit x at K <= 4096: 4 rows, so that the chunks run on the stream
-    // kernel, not the row-run kernel.  Same box, g64, us per launch, M = 8,
-    // K = 2048, N = 8192: 3-bit 55.9 -> 16.2, 2-bit 56.0 -> 15.4; M = 6, K =
-    // 3072, N = 14336, 5-bit 83.9 -> 26.0; 8-bit N = 8192 60.7 -> 14.9)
-    int chunk = args.x_dtype == DT_F32 || args.K <= 4096 ? 4 : 8;
-    while (chunk > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) chunk >>= 1;
-    // one row of x may still run on the split-K stream kernel (K <= 32768),
-    // which stages x in up to 160 KB; the row-run kernel declines it itself
-    if (args.M > 1 && gemv_lds_bytes(chunk, args.K, args.x_dtype) > 64 * 1024) return LuxStatus::NotSupported;
-    for (int m0 = 0; m0 < args.M; m0 += chunk) {
-        const LuxStatus s = launch_bits(rows(m0, args.M - m0 < chunk ? args.M - m0 : chunk), st);
+    // the rest (16-bit x at K <= 4096: 3/5/6-bit codes and the shapes the
+    // kernels above decline): chunks of 4 rows on the stream kernel, the last
+    // one 1..4 rows.  They ran in one launch of a row-run kernel with up to 8
+    // rows of x staged in LDS, since retired (same box, g64, us per launch,
+    // M = 8, K = 2048, N = 8192: 3-bit 55.9 -> 16.2, 2-bit 56.0 -> 15.4; M =
+    // 6, K = 3072, N = 14336, 5-bit 83.9 -> 26.0; 8-bit N = 8192 60.7 ->
+    // 14.9).  Anything else is NotSupported here: the generic kernel.
+    for (int m0 = 0; m0 < args.M; m0 += 4) {
+        const LuxStatus s = launch_bits(rows(m0, args.M - m0 < 4 ? args.M - m0 : 4), st);
         if (s != LuxStatus::Ok) return s;
     }
     return LuxStatus::Ok;

@@ -1,6 +1,8 @@
-// qgemv_impl.h -- bandwidth-bound dequant-GEMV for small M (gfx950): kernel templates.
+// qgemv_impl.h -- bandwidth-bound dequant-GEMV for small M (gfx950): the
+// stream and split-K kernels, the helpers the other GEMV kernels share, and
+// the per-bit-width launcher (launch_m).
 //
-// y[m, n] = sum_k x[m, k] * (s[n,g] * q[n,k] + b[n,g]),  m < M <= 8.
+// y[m, n] = sum_k x[m, k] * (s[n,g] * q[n,k] + b[n,g]).
 //
 // Work split: a wave owns a run of rows n; its 64 lanes split K.  Lane l of
 // the wave takes "unit" u = l (+64, +128, ... for K > 4096) of every row: 64
@@ -13,191 +15,13 @@
 // (one shift + one v_and_or_b32 per pair for BITS 2/4/8), multiplied with x by
 // v_dot2_f32_{f16,bf16} in fp32.  Per group
 //     s*sum x q + b*sum x  =  (s*2^BITS) * sum x v(q)  +  (b - s*2^BITS) * xs,
-// xs = sum of x over the group, computed once per block.  fp32 activations
-// use plain fp32 FMAs.  Lane partials are reduced with DPP row operations and
-// readlane (no LDS).
+// xs = sum of x over the group.  fp32 activations use plain fp32 FMAs.
 #pragma once
 #include "kernels.h"
 #include "qcommon.h"
 
 namespace lxq {
 namespace gemv {
-
-constexpr int kThreads = 256;  // 4 waves
-
-template <int TX>
-struct XLds {
-    static constexpr int kElem = (TX == DT_F32) ? 4 : 2;
-    // one 64-code unit = 64 elements + padding so that ds_read_b128 of
-    // consecutive lanes spread over the LDS banks
-    static constexpr int kUnitStride = (TX == DT_F32) ? 68 : 72;  // elements
-};
-
-template <int BITS>
-__device__ __forceinline__ void load_unit(const uint32_t* __restrict__ p, uint32_t* w) {
-    constexpr int W = 2 * BITS;
-#pragma unroll
-    for (int i = 0; i + 4 <= W; i += 4) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(p + i);
-        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
-    }
-    if constexpr (W % 4 == 2) {
-        u32x2 v = *reinterpret_cast<const u32x2*>(p + (W - 2));
-        w[W - 2] = v.x; w[W - 1] = v.y;
-    }
-}
-
-template <int BITS, int TX, int MR, int RU, bool EPI>
-__global__ __launch_bounds__(kThreads) void qgemv_kernel(
-    const void* __restrict__ x, const uint32_t* __restrict__ wq, const void* __restrict__ scales,
-    const void* __restrict__ biases, void* __restrict__ y, int M, int K, int N, int gsize,
-    int sb_dt, Epilogue ep, int rows_per_wave) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    using XL = XLds<TX>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int units = K >> 6;
-    const int slabs = (units + 63) >> 6;
-    const int G = K / gsize;
-    const int row_words = (K * BITS) >> 5;
-    const int x_row_elems = units * XL::kUnitStride;
-    float* xs_lds = reinterpret_cast<float*>(smem + (size_t)MR * x_row_elems * XL::kElem);
-
-    constexpr float kPow = MagicCfg<BITS, (TX == DT_F16 ? 10 : 7)>::kPow;
-    // bf16 cannot hold 1 + q/256: 8-bit codes with bf16 x use v(q) = q
-    constexpr bool kMagic = (TX != DT_F32) && !(TX == DT_BF16 && BITS == 8);
-    // x order matches the operand pairing of the codes
-    constexpr bool kApartX = kMagic && PairLayout<BITS>::kApart;
-
-    // ---- stage x[M][K] into LDS (slot order + padding) and group sums ----
-    for (int idx = threadIdx.x; idx < M * K; idx += kThreads) {
-        const int m = idx / K, k = idx - m * K;
-        const int u = k >> 6, c = k & 63;
-        const int dst = m * x_row_elems + u * XL::kUnitStride + (kApartX ? x_slot<BITS>(c) : c);
-        if constexpr (TX == DT_F32)
-            reinterpret_cast<float*>(smem)[dst] = reinterpret_cast<const float*>(x)[idx];
-        else
-            reinterpret_cast<uint16_t*>(smem)[dst] = reinterpret_cast<const uint16_t*>(x)[idx];
-    }
-    // sums of x over every 32-code half unit: the bias term of a group is
-    // b * (sum of x over the group) and a unit covers 2 halves
-    const int H = K >> 5;
-    for (int idx = threadIdx.x; idx < M * H; idx += kThreads) {
-        const int m = idx / H, h = idx - m * H;
-        float s = 0.f;
-        for (int k = h * 32; k < h * 32 + 32; k++) s += load_f(x, (size_t)m * K + k, TX);
-        xs_lds[idx] = s;
-    }
-    __syncthreads();
-
-    const int n_begin = (blockIdx.x * (kThreads / 64) + wave) * rows_per_wave;
-    const int n_end = min(N, n_begin + rows_per_wave);
-
-    for (int n0 = n_begin; n0 < n_end; n0 += RU) {
-        float acc[RU][MR];
-#pragma unroll
-        for (int r = 0; r < RU; r++)
-#pragma unroll
-            for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
-
-        for (int sl = 0; sl < slabs; sl++) {
-            const int u = sl * 64 + lane;
-            const bool active = u < units;
-            const int g0 = (u * 64) / gsize;
-            uint32_t wv[RU][2 * BITS];
-            float sc[RU][2], bi[RU][2];
-            // issue all loads of the batch first (memory-level parallelism)
-#pragma unroll
-            for (int r = 0; r < RU; r++) {
-                const int n = n0 + r;
-                if (active && n < n_end) {
-                    load_unit<BITS>(wq + (size_t)n * row_words + (size_t)u * 2 * BITS, wv[r]);
-                    sc[r][0] = load_f(scales, (size_t)n * G + g0, sb_dt);
-                    bi[r][0] = load_f(biases, (size_t)n * G + g0, sb_dt);
-                    if (gsize == 32) {
-                        sc[r][1] = load_f(scales, (size_t)n * G + g0 + 1, sb_dt);
-                        bi[r][1] = load_f(biases, (size_t)n * G + g0 + 1, sb_dt);
-                    } else {
-                        sc[r][1] = sc[r][0];
-                        bi[r][1] = bi[r][0];
-                    }
-                }
-            }
-            if (!active) continue;
-#pragma unroll
-            for (int r = 0; r < RU; r++) {
-                const int n = n0 + r;
-                if (n >= n_end) continue;
-                // per m: D0, D1 = sums over the two 32-code halves of the unit
-                if constexpr (TX == DT_F32) {
-                    float q[64];
-#pragma unroll
-                    for (int i = 0; i < 64; i++) q[i] = (float)unit_code<BITS>(wv[r], i);
-#pragma unroll
-                    for (int m = 0; m < MR; m++) {
-                        if (m >= M) break;
-                        const float* xl = reinterpret_cast<const float*>(smem) +
-                                          m * x_row_elems + u * XL::kUnitStride;
-                        float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-                        for (int i = 0; i < 32; i++) d0 = fmaf(xl[i], q[i], d0);
-#pragma unroll
-                        for (int i = 32; i < 64; i++) d1 = fmaf(xl[i], q[i], d1);
-                        const float h0 = xs_lds[m * H + 2 * u], h1 = xs_lds[m * H + 2 * u + 1];
-                        acc[r][m] += (sc[r][0] * d0 + bi[r][0] * h0) + (sc[r][1] * d1 + bi[r][1] * h1);
-                    }
-                } else {
-                    uint32_t pr[32];
-                    if constexpr (kMagic)
-                        unit_pairs_magic<BITS, (TX == DT_F16 ? 10 : 7)>(wv[r], pr);
-                    else
-                        unit_pairs_bf16_u8(wv[r], pr);
-#pragma unroll
-                    for (int m = 0; m < MR; m++) {
-                        if (m >= M) break;
-                        const u32x4* xl = reinterpret_cast<const u32x4*>(
-                            reinterpret_cast<const uint16_t*>(smem) + m * x_row_elems +
-                            u * XL::kUnitStride);
-                        float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            u32x4 xv = xl[i];
-                            d0 = dot2(xv.x, pr[4 * i], d0, TX);
-                            d0 = dot2(xv.y, pr[4 * i + 1], d0, TX);
-                            d0 = dot2(xv.z, pr[4 * i + 2], d0, TX);
-                            d0 = dot2(xv.w, pr[4 * i + 3], d0, TX);
-                        }
-#pragma unroll
-                        for (int i = 4; i < 8; i++) {
-                            u32x4 xv = xl[i];
-                            d1 = dot2(xv.x, pr[4 * i], d1, TX);
-                            d1 = dot2(xv.y, pr[4 * i + 1], d1, TX);
-                            d1 = dot2(xv.z, pr[4 * i + 2], d1, TX);
-                            d1 = dot2(xv.w, pr[4 * i + 3], d1, TX);
-                        }
-                        const float h0 = xs_lds[m * H + 2 * u], h1 = xs_lds[m * H + 2 * u + 1];
-                        if constexpr (kMagic) {
-                            // D = sum x v(q) = h + 2^-B sum x q  =>
-                            // s sum x q + b h = (s 2^B) D + (b - s 2^B) h
-                            acc[r][m] += ((sc[r][0] * kPow) * d0 + fmaf(-sc[r][0], kPow, bi[r][0]) * h0) +
-                                         ((sc[r][1] * kPow) * d1 + fmaf(-sc[r][1], kPow, bi[r][1]) * h1);
-                        } else {
-                            acc[r][m] += (sc[r][0] * d0 + bi[r][0] * h0) + (sc[r][1] * d1 + bi[r][1] * h1);
-                        }
-                    }
-                }
-            }
-        }
-        // ---- reduce lane partials and store ----
-#pragma unroll
-        for (int r = 0; r < RU; r++) {
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                const float v = wave_sum(acc[r][m]);
-                if (lane == 0 && m < M && n0 + r < n_end) store_out<EPI>(y, (size_t)m * N + n0 + r, n0 + r, ep, v);
-            }
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Streaming kernel for K <= 4096 (one 64-code unit per lane): M <= 4 with
@@ -904,38 +728,6 @@ LuxStatus launch_split(const QmmArgs& a, hipStream_t st) {
     }
 }
 
-template <int BITS, int TX, int MR, bool EPI>
-LuxStatus launch_t_e(const QmmArgs& a, hipStream_t st) {
-    constexpr int RU = 4;
-    using XL = XLds<TX>;
-    const int units = a.K / 64;
-    const size_t lds = (size_t)MR * units * XL::kUnitStride * XL::kElem + (size_t)MR * (a.K / 32) * 4;
-    if (lds > 64 * 1024) return LuxStatus::NotSupported;
-    (void)units;
-    // rows per wave: enough waves to cover the chip several times over
-    const int waves_wanted = 256 * 8;
-    int rpw = (a.N + waves_wanted - 1) / waves_wanted;
-    rpw = ((rpw + RU - 1) / RU) * RU;
-    if (rpw < RU) rpw = RU;
-    const int waves = (a.N + rpw - 1) / rpw;
-    const int blocks = (waves + 3) / 4;
-    if (planned(a, "qgemv_kernel")) return LuxStatus::Ok;
-    auto kern = qgemv_kernel<BITS, TX, MR, RU, EPI>;
-    // once per instantiation; a function-local static initializes exactly once
-    // even when several threads make the first call together
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-    if (attr != hipSuccess) return LuxStatus::Internal;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, a.x, a.wq, a.scales, a.biases,
-                       a.y, a.M, a.K, a.N, a.group_size, a.sb_dtype, a.epi(), rpw);
-    return hipGetLastError() == hipSuccess ? LuxStatus::Ok : LuxStatus::Internal;
-}
-
-template <int BITS, int TX, int MR>
-LuxStatus launch_t(const QmmArgs& a, hipStream_t st) {
-    return a.has_epilogue() ? launch_t_e<BITS, TX, MR, true>(a, st) : launch_t_e<BITS, TX, MR, false>(a, st);
-}
-
 // M == 1, K <= 4096: the whole-line kernel of qgemv_line.h (defined there,
 // instantiated by the per-bit-width translation units); NotSupported for
 // shapes it does not take
@@ -971,13 +763,7 @@ LuxStatus launch_m(const QmmArgs& a, hipStream_t st) {
             return launch_stream_r<BITS, TX, 4>(a, st);
         }
     }
-    if (a.M <= 1) return launch_t<BITS, TX, 1>(a, st);
-    if (a.M <= 2) return launch_t<BITS, TX, 2>(a, st);
-    if (a.M <= 4) return launch_t<BITS, TX, 4>(a, st);
-    // f32 x comes in chunks of at most 4 rows: 8 rows of f32 x spilled
-    // 500-700 VGPRs to scratch
-    if constexpr (TX == DT_F32) return LuxStatus::NotSupported;
-    else return launch_t<BITS, TX, 8>(a, st);
+    return LuxStatus::NotSupported;
 }
 
 template <int BITS>

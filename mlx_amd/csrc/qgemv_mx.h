@@ -302,9 +302,9 @@ LuxStatus launch_mx_m(const QmmArgs& a, hipStream_t st) {
 //    M >= 3 (K = 8192: 14.2 against 15.8; K = 6144 M = 3: 11.1 against 14.7)
 //    and the LDS-ring kernel 8-bit M >= 3 (K = 8192 g128 bf16 M = 4: 20.3
 //    against 24.2).
-//  * f32 x: everywhere it applies.  The only other kernel for f32 x at
-//    M >= 2 is the row-run fallback, 5-6x slower (M = 4, K = N = 4096, 4-bit:
-//    33.0 us).
+//  * f32 x: everywhere it applies.  The alternative for f32 x at M >= 2 is
+//    one M = 1 launch per row (the row-run kernel it replaced was 5-6x slower:
+//    M = 4, K = N = 4096, 4-bit: 33.0 us).
 inline bool mx_wins(int bits, int M, int x_dtype, int K) {
     if (x_dtype == DT_F32 || K > 8192) return true;
     if (K > 4096) return M == 2 || bits == 2;
