@@ -135,8 +135,8 @@ def test_row_split_long_k_parity(ctx, oracle, xd, sbd, od):
 @pytest.mark.parametrize("xd,sbd,od", [(F16, F16, F16), (BF16, BF16, BF16), (F16, F32, F32), (BF16, F16, F32)])
 def test_split_k_row_pairs_parity(ctx, oracle, xd, sbd, od):
     """16-bit x, K > 4096, M = 3..8 where no M-wide kernel takes the shape
-    (3/5/6-bit codes; K % 1024 != 0 for 4/8-bit; K beyond the row-run
-    kernel's x staging): pairs of rows on the split-K kernel, a last single
+    (3/5/6-bit codes; K % 1024 != 0 for 4/8-bit; K up to 32768): pairs of
+    rows on the split-K kernel, a last single
     row on the M = 1 split-K kernel, each launch writing its own rows of y;
     K up to 32768, ragged N, every group size."""
     O = oracle
@@ -849,7 +849,7 @@ FUSED_CASES = [
     (6, 11008, 72, 4, 64, BF16),    # rows 0..3 and 4..5 as two launches (two-chunk decode)
     (2, 4096, 40, 4, 64, F16),      # K-split whole-line GEMV (two rows of x)
     (2, 4096, 40, 3, 64, F16),      # stream GEMV (two rows of x, 3-bit)
-    (6, 960, 70, 3, 64, F16),       # row-run GEMV (3-bit, K % 1024 != 0)
+    (6, 960, 70, 3, 64, F16),       # stream GEMV in chunks of 4 rows (3-bit, K % 1024 != 0)
     (3, 1024, 50, 6, 64, F32),      # whole-line GEMV once per row (f32 x, 6-bit)
     (6, 512, 96, 4, 64, BF16),      # skinny MFMA GEMV
     (3, 1024, 72, 8, 128, BF16),    # K-split whole-line GEMV (three rows of x, 8-bit)
@@ -966,7 +966,8 @@ def test_weights_past_2gib(ctx, oracle):
     2 GiB + 8 MB): the GEMV kernels address them with per-block buffer
     bases, the size-limited kernels decline them, and every sampled row --
     the first ones, rows around the 2^31-byte mark, the last block -- equals
-    the oracle for M = 1 and 3 (stream kernel), 6 (row-run kernel) and 96
+    the oracle for M = 1 (whole-line kernel), 3 and 6 (stream kernel, 6 in
+    chunks of 4 rows) and 96
     (the large GEMM, whose 32-bit offsets reach 4 GiB)."""
     O = oracle
     K, gs, bits = 4096, 64, 4

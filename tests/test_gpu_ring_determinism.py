@@ -143,8 +143,9 @@ def test_split_k_and_lds_gemm_repeat(ctx, bits, sbd):
 @pytest.mark.parametrize("sbd", SB, ids=["sb_f16", "sb_bf16", "sb_f32"])
 def test_gemv_repeat(ctx, bits, sbd):
     """The GEMV kernels AUTO picks for M = 1..8 (whole-line, split-K,
-    decode, 4x4x4-MFMA, K-split whole-line, stream, skinny and row-run
-    kernels; several stage x or partial sums in LDS behind barriers), group
+    decode, 4x4x4-MFMA, K-split whole-line, stream and skinny kernels, and
+    rows split over launches; several stage x or partial sums in LDS behind
+    barriers), group
     sizes 32 and 128, K = 4096 and 14336, ragged N = 4100."""
     xd = BF16 if sbd == BF16 else F16
     for gs in (32, 128):
